@@ -1,0 +1,531 @@
+// (a4, a5, a6) Mixed draft/verify paged attention for gfx950.
+//
+// One wave processes one (row, kv head) segment piece at a time: all
+// q_len * group query rows of the GQA group against a contiguous range of
+// the segment's 16-token pages. Per page and lane (r = lane % 16 selects a
+// key / query row, grp = lane / 16 a 32-dim slice):
+//   * K and V: lane reads 64 contiguous bytes (4 x 128-bit loads each) of key
+//     r, dims [32*grp, 32*grp + 32): one wave instruction covers 16 rows x
+//     64 B, four cover the page-head's 4 KB;
+//   * S^T = K . Q^T with 4 v_mfma_f32_16x16x32_bf16 (A = K rows straight from
+//     registers, B = the row's Q slice; the MFMA sums over k in any order both
+//     operands agree on, so the 64-byte lane slice needs no shuffle). Lane
+//     holds S^T[key 4*grp + i][row r], which is already the B operand layout
+//     of the P.V product;
+//   * V is transposed in registers by an exact MFMA against the identity
+//     (8 x v_mfma_f32_16x16x16_bf16): lane then holds V[keys 4*grp..+3][dim]
+//     as the A operand of O^T = V^T . P^T, and the O^T accumulator of lane l
+//     covers row r, dims 32*grp + 4*vt + i -- its own contiguous 64 B of
+//     output;
+//   * online softmax in fp32 with exp2 and a base-2 LSE; the row max is
+//     reduced across the 4 lane groups with two xor shuffles.
+// No LDS is used. K/V stream through one 32-VGPR register buffer pipelined at
+// half-page granularity (the next page's K is requested once QK^T has consumed
+// K, its V once P.V has consumed V). A row tile is 16 query rows; NT tiles
+// share the K/V registers (q_len * group <= 16 * NT).
+#include "common.h"
+
+namespace aspire {
+namespace {
+
+struct AttnParams {
+  const uint16_t* q;
+  int64_t q_st, q_sh;
+  const uint16_t* cache;
+  int64_t c_sp, c_skv, c_st, c_sh;
+  const int32_t* kv_indices;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  float* lse;
+  const int32_t* plan;
+  int64_t indptr_off, items_off;
+  int32_t num_waves;
+  float* part_o;
+  float* part_lse;
+  int32_t hq, hkv, group;
+  float scale_log2;
+  int32_t causal;
+  void* dump;
+  int32_t dump_kind, dump_f32;
+  int64_t dump_stride;
+  int32_t dump_heads;
+  const int32_t* dump_flags;
+  float* page_scores;
+  int64_t ps_stride;
+};
+
+struct MergeParams {
+  const int32_t* plan;
+  int64_t merge_off;
+  const float* part_o;
+  const float* part_lse;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  float* lse;
+  int32_t hq, group;
+};
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+#ifndef ASPIRE_NT1_WAVES
+#define ASPIRE_NT1_WAVES 3
+#endif
+
+__device__ __forceinline__ void load_k(const AttnParams& p, int64_t phys, int g, int r, int grp,
+                                       bool key_ok, uint4 (&dst)[4]) {
+  const uint16_t* kp = p.cache + phys * p.c_sp + int64_t(r) * p.c_st + int64_t(g) * p.c_sh + grp * 32;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    dst[c] = key_ok ? reinterpret_cast<const uint4*>(kp)[c] : make_uint4(0, 0, 0, 0);
+}
+
+__device__ __forceinline__ void load_v(const AttnParams& p, int64_t phys, int g, int r, int grp,
+                                       bool key_ok, uint4 (&dst)[4]) {
+  const uint16_t* vp =
+      p.cache + phys * p.c_sp + p.c_skv + int64_t(r) * p.c_st + int64_t(g) * p.c_sh + grp * 32;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    dst[c] = key_ok ? reinterpret_cast<const uint4*>(vp)[c] : make_uint4(0, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) {
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+__device__ __forceinline__ i16x4 as_i16x4(uint32_t a, uint32_t b) {
+  uint2 u = make_uint2(a, b);
+  return __builtin_bit_cast(i16x4, u);
+}
+
+__device__ __forceinline__ void store_dump(const AttnParams& p, int64_t idx, float v) {
+  if (p.dump_f32) {
+    static_cast<float*>(p.dump)[idx] = v;
+  } else {
+    _Float16 h = static_cast<_Float16>(v);
+    static_cast<_Float16*>(p.dump)[idx] = h;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it, int lane,
+                                         i16x4 ident) {
+  const int r = lane & 15;
+  const int grp = lane >> 4;
+  const int G = p.group;
+  const int b = it.bg >> 8;
+  const int g = it.bg & 255;
+  const int rows = it.q_len * G;
+  const int kv_len = it.kv_len;
+
+  // Query fragments and per-row causal limits.
+  bf16x8 qf[NT][4];
+  int limit[NT];
+  int row_qi[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int row = t * 16 + r;
+    if (row < rows) {
+      const int qi = row / G;
+      const int hh = row - qi * G;
+      const uint16_t* src =
+          p.q + int64_t(it.q_start + qi) * p.q_st + int64_t(g * G + hh) * p.q_sh + grp * 32;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qf[t][c] = as_bf16x8(reinterpret_cast<const uint4*>(src)[c]);
+      limit[t] = p.causal ? min(kv_len - it.q_len + qi, kv_len - 1) : kv_len - 1;
+      row_qi[t] = qi;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qf[t][c] = as_bf16x8(make_uint4(0, 0, 0, 0));
+      limit[t] = -1;
+      row_qi[t] = -1;
+    }
+  }
+
+  float m[NT], l[NT];
+  f32x4 acc[NT][8];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    m[t] = kNegInf;
+    l[t] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const bool do_dump = p.dump_kind != 0 && (p.dump_flags == nullptr || p.dump_flags[b] != 0);
+  const bool do_score = p.page_scores != nullptr && it.q_len == 1;
+  const int dump_slots = p.dump_kind == 2 ? 2 : 1;
+
+  // Page ids are fetched 64 at a time (one per lane) and broadcast with readlane.
+  const int pb = it.page_begin;
+  const int pe = it.page_end;
+  int win_base = pb;
+  int win = (pb + lane < pe) ? p.kv_indices[it.list_base + pb + lane] : 0;
+  auto page_id = [&](int pg) -> int64_t {
+    if (pg - win_base >= 64) {
+      win_base = pg;
+      win = (pg + lane < pe) ? p.kv_indices[it.list_base + pg + lane] : 0;
+    }
+    return int64_t(__builtin_amdgcn_readlane(win, pg - win_base));
+  };
+
+  // Single K/V register buffer, pipelined at half-page granularity: the next
+  // page's K is requested as soon as this page's QK^T has consumed K, and its V
+  // as soon as P.V has consumed V, so about one page stays in flight per wave
+  // with 32 VGPRs of staging.
+  uint4 kr[4], vr[4];
+  if (pb < pe) {
+    const int64_t phys = page_id(pb);
+    const bool ok = pb * 16 + r < kv_len;
+    load_k(p, phys, g, r, grp, ok, kr);
+    load_v(p, phys, g, r, grp, ok, vr);
+  }
+  for (int pg = pb; pg < pe; ++pg) {
+    const bool has_next = pg + 1 < pe;
+    const int64_t next_phys = has_next ? page_id(pg + 1) : 0;
+    const bool next_ok = (pg + 1) * 16 + r < kv_len;
+    const int base_pos = pg * 16 + grp * 4;
+
+    f32x4 s[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s[t] = mfma_16x16x32_bf16(as_bf16x8(kr[c]), qf[t][c], s[t]);
+    }
+    if (has_next) load_k(p, next_phys, g, r, grp, next_ok, kr);
+
+    i16x4 pf[NT];
+    float alpha[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (do_dump && row_qi[t] >= 0) {
+        const int qi = row_qi[t];
+        int slot = -1;
+        if (p.dump_kind == 2)
+          slot = qi == 0 ? 0 : (qi == it.q_len - 1 ? 1 : -1);
+        else if (qi == it.q_len - 1)
+          slot = 0;
+        if (slot >= 0) {
+          const int head = g * G + (t * 16 + r - qi * G);
+          const int64_t base =
+              (int64_t(b * p.dump_heads + head) * dump_slots + slot) * p.dump_stride;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (base_pos + i < kv_len) store_dump(p, base + base_pos + i, s[t][i]);
+        }
+      }
+      if (do_score && t == 0) {
+        float rs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rs += (base_pos + i < kv_len) ? s[t][i] : 0.f;
+        rs += shfl_xor_f(rs, 16);
+        rs += shfl_xor_f(rs, 32);
+        const int cnt = min(16, kv_len - pg * 16);
+        float val = (r < G) ? rs / float(cnt) : kNegInf;
+        val = fmaxf(val, shfl_xor_f(val, 1));
+        val = fmaxf(val, shfl_xor_f(val, 2));
+        val = fmaxf(val, shfl_xor_f(val, 4));
+        val = fmaxf(val, shfl_xor_f(val, 8));
+        if (lane == 0) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + pg] = val;
+      }
+
+      float x[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        x[i] = (base_pos + i <= limit[t]) ? s[t][i] * p.scale_log2 : kNegInf;
+      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      mx = fmaxf(mx, shfl_xor_f(mx, 16));
+      mx = fmaxf(mx, shfl_xor_f(mx, 32));
+      const float m_new = fmaxf(m[t], mx);
+      float a = 1.f;
+      float pv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (m_new != kNegInf) {
+        a = __builtin_amdgcn_exp2f(m[t] - m_new);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+      }
+      l[t] = l[t] * a + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+      m[t] = m_new;
+      alpha[t] = a;
+      pf[t] = as_i16x4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]));
+    }
+
+    // O^T += V^T P^T, one 16-dim slice at a time: transpose the slice with an
+    // exact identity MFMA (the values are bf16 already), then accumulate.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint4 src = vr[j >> 1];
+      const i16x4 va = (j & 1) ? as_i16x4(src.z, src.w) : as_i16x4(src.x, src.y);
+      const f32x4 d = mfma_16x16x16_bf16(va, ident, f32x4{0.f, 0.f, 0.f, 0.f});
+      const i16x4 vt = as_i16x4(pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3]));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t][j] = mfma_16x16x16_bf16(vt, pf[t], acc[t][j] * alpha[t]);
+    }
+    if (has_next) load_v(p, next_phys, g, r, grp, next_ok, vr);
+  }
+
+  // Epilogue: normalise and write the final output or the fp32 partial.
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float lt = l[t];
+    lt += shfl_xor_f(lt, 16);
+    lt += shfl_xor_f(lt, 32);
+    const int row = t * 16 + r;
+    if (row >= rows) continue;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const float lse_v = lt > 0.f ? m[t] + __builtin_log2f(lt) : kNegInf;
+    if (it.partial_row < 0) {
+      const int qi = row / G;
+      const int head = g * G + (row - qi * G);
+      const int token = it.q_start + qi;
+      uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + grp * 32;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 a0 = acc[t][2 * c];
+        const f32x4 a1 = acc[t][2 * c + 1];
+        uint4 w;
+        w.x = pack_bf16x2_rne(a0[0] * inv, a0[1] * inv);
+        w.y = pack_bf16x2_rne(a0[2] * inv, a0[3] * inv);
+        w.z = pack_bf16x2_rne(a1[0] * inv, a1[1] * inv);
+        w.w = pack_bf16x2_rne(a1[2] * inv, a1[3] * inv);
+        reinterpret_cast<uint4*>(dst)[c] = w;
+      }
+      if (grp == 0 && p.lse != nullptr) p.lse[int64_t(token) * p.hq + head] = lse_v;
+    } else {
+      const int64_t prow = int64_t(it.partial_row) + row;
+      float* dst = p.part_o + prow * kHeadDim + grp * 32;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const f32x4 a = acc[t][j];
+        reinterpret_cast<float4*>(dst)[j] = make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+      }
+      if (grp == 0) p.part_lse[prow] = lse_v;
+    }
+  }
+}
+
+// Waves per SIMD the register allocation must allow: the kernel is bound by
+// bytes in flight, so occupancy is worth more than spare registers.
+template <int NT>
+struct Occupancy {
+  static constexpr int waves = NT == 1 ? ASPIRE_NT1_WAVES : 2;
+};
+
+template <int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Occupancy<NT>::waves)))
+void attention_kernel(AttnParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (wave >= p.num_waves) return;
+  const int32_t* indptr = p.plan + p.indptr_off;
+  const int w0 = wave_uniform(indptr[wave]);
+  const int w1 = wave_uniform(indptr[wave + 1]);
+  if (w0 >= w1) return;
+  // Identity B operand: lane holds B[k = 4*grp + j][n = r] = (k == n).
+  const int r = lane & 15, grp = lane >> 4;
+  const uint32_t one = 0x3f80u;  // bf16 1.0
+  uint32_t e0 = (4 * grp + 0 == r ? one : 0u) | ((4 * grp + 1 == r ? one : 0u) << 16);
+  uint32_t e1 = (4 * grp + 2 == r ? one : 0u) | ((4 * grp + 3 == r ? one : 0u) << 16);
+  const i16x4 ident = as_i16x4(e0, e1);
+  const WorkItem* items = reinterpret_cast<const WorkItem*>(p.plan + p.items_off);
+  for (int w = w0; w < w1; ++w) {
+    WorkItem it;
+    it.q_start = wave_uniform(items[w].q_start);
+    it.q_len = wave_uniform(items[w].q_len);
+    it.kv_len = wave_uniform(items[w].kv_len);
+    it.list_base = wave_uniform(items[w].list_base);
+    it.page_begin = wave_uniform(items[w].page_begin);
+    it.page_end = wave_uniform(items[w].page_end);
+    it.bg = wave_uniform(items[w].bg);
+    it.partial_row = wave_uniform(items[w].partial_row);
+    run_item<NT>(p, it, lane, ident);
+  }
+}
+
+// Merge of split segments: thread e of a merge item handles 4 dims of one row.
+__global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
+  const int num_merge = p.plan[3];
+  const MergeItem* items = reinterpret_cast<const MergeItem*>(p.plan + p.merge_off);
+  for (int mi = blockIdx.x; mi < num_merge; mi += gridDim.x) {
+    const MergeItem it = items[mi];
+    const int g = it.bg & 255;
+    for (int e = threadIdx.x; e < it.rows * 32; e += blockDim.x) {
+      const int row = e >> 5;
+      const int d4 = (e & 31) * 4;
+      float mx = kNegInf;
+      for (int k = 0; k < it.num_pieces; ++k)
+        mx = fmaxf(mx, p.part_lse[int64_t(it.first_partial_row) + int64_t(k) * it.rows + row]);
+      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f, sum = 0.f;
+      if (mx != kNegInf) {
+        for (int k = 0; k < it.num_pieces; ++k) {
+          const int64_t pr = int64_t(it.first_partial_row) + int64_t(k) * it.rows + row;
+          const float w = __builtin_amdgcn_exp2f(p.part_lse[pr] - mx);
+          const float4 v = *reinterpret_cast<const float4*>(p.part_o + pr * kHeadDim + d4);
+          sum += w;
+          o0 += w * v.x;
+          o1 += w * v.y;
+          o2 += w * v.z;
+          o3 += w * v.w;
+        }
+      }
+      const float inv = sum > 0.f ? 1.f / sum : 0.f;
+      const int qi = row / p.group;
+      const int head = g * p.group + (row - qi * p.group);
+      const int token = it.q_start + qi;
+      uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + d4;
+      uint2 w2;
+      w2.x = pack_bf16x2_rne(o0 * inv, o1 * inv);
+      w2.y = pack_bf16x2_rne(o2 * inv, o3 * inv);
+      *reinterpret_cast<uint2*>(dst) = w2;
+      if (d4 == 0 && p.lse != nullptr)
+        p.lse[int64_t(token) * p.hq + head] = sum > 0.f ? mx + __builtin_log2f(sum) : kNegInf;
+    }
+  }
+}
+
+// Standalone state merge: one thread per (row, 4 dims).
+__global__ __launch_bounds__(256) void merge_states_kernel(const float* v, const float* s, int n,
+                                                           int64_t rows, void* v_out, int out_bf16,
+                                                           float* s_out) {
+  const int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (e >= rows * 32) return;
+  const int64_t row = e >> 5;
+  const int d4 = int(e & 31) * 4;
+  float mx = kNegInf;
+  for (int k = 0; k < n; ++k) mx = fmaxf(mx, s[int64_t(k) * rows + row]);
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  float sum = 0.f;
+  if (mx != kNegInf) {
+    for (int k = 0; k < n; ++k) {
+      const float w = __builtin_amdgcn_exp2f(s[int64_t(k) * rows + row] - mx);
+      const float4 x = *reinterpret_cast<const float4*>(v + (int64_t(k) * rows + row) * kHeadDim + d4);
+      sum += w;
+      o[0] += w * x.x;
+      o[1] += w * x.y;
+      o[2] += w * x.z;
+      o[3] += w * x.w;
+    }
+  }
+  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+  if (out_bf16) {
+    uint2 w2;
+    w2.x = pack_bf16x2_rne(o[0] * inv, o[1] * inv);
+    w2.y = pack_bf16x2_rne(o[2] * inv, o[3] * inv);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(v_out) + row * kHeadDim + d4) = w2;
+  } else {
+    *reinterpret_cast<float4*>(static_cast<float*>(v_out) + row * kHeadDim + d4) =
+        make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+  }
+  if (d4 == 0 && s_out != nullptr) s_out[row] = sum > 0.f ? mx + __builtin_log2f(sum) : kNegInf;
+}
+
+inline bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+}  // namespace aspire
+
+extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
+                                    const aspire_attention_args* a, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(layout && a, "null argument");
+  ASPIRE_CHECK_ARG(a->head_dim == kHeadDim, "head_dim must be 128");
+  ASPIRE_CHECK_ARG(a->page_size == kPage, "page_size must be 16");
+  ASPIRE_CHECK_ARG(a->num_kv_heads > 0 && a->num_kv_heads < 256 &&
+                       a->num_qo_heads % a->num_kv_heads == 0,
+                   "bad head counts");
+  ASPIRE_CHECK_ARG(a->q && a->kv_cache && a->kv_indices && a->out && a->plan_dev && a->float_ws,
+                   "null pointer");
+  ASPIRE_CHECK_ARG(al16(a->q) && al16(a->kv_cache) && al16(a->out) && al16(a->float_ws),
+                   "q, kv_cache, out and the float workspace must be 16-byte aligned");
+  ASPIRE_CHECK_ARG(a->q_stride_t % 8 == 0 && a->q_stride_h % 8 == 0 && a->out_stride_t % 8 == 0 &&
+                       a->out_stride_h % 8 == 0 && a->cache_stride_p % 8 == 0 &&
+                       a->cache_stride_kv % 8 == 0 && a->cache_stride_t % 8 == 0 &&
+                       a->cache_stride_h % 8 == 0,
+                   "strides must be multiples of 8 elements");
+  ASPIRE_CHECK_ARG(a->dump_kind >= 0 && a->dump_kind <= 2, "dump_kind must be 0, 1 or 2");
+  ASPIRE_CHECK_ARG(a->dump_kind == 0 || (a->dump != nullptr && a->dump_kv_stride > 0 &&
+                                         a->dump_num_heads > 0),
+                   "dump buffer, stride and head count required");
+  const PlanOffsets off = plan_offsets(*layout);
+  AttnParams p;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.q_st = a->q_stride_t;
+  p.q_sh = a->q_stride_h;
+  p.cache = static_cast<const uint16_t*>(a->kv_cache);
+  p.c_sp = a->cache_stride_p;
+  p.c_skv = a->cache_stride_kv;
+  p.c_st = a->cache_stride_t;
+  p.c_sh = a->cache_stride_h;
+  p.kv_indices = a->kv_indices;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.o_st = a->out_stride_t;
+  p.o_sh = a->out_stride_h;
+  p.lse = a->lse;
+  p.plan = static_cast<const int32_t*>(a->plan_dev);
+  p.num_waves = layout->num_waves;
+  p.part_o = a->float_ws;
+  p.part_lse = a->float_ws + layout->partial_rows_cap * kHeadDim;
+  p.hq = a->num_qo_heads;
+  p.hkv = a->num_kv_heads;
+  p.group = a->num_qo_heads / a->num_kv_heads;
+  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p.causal = a->causal;
+  p.dump = a->dump;
+  p.dump_kind = a->dump_kind;
+  p.dump_f32 = a->dump_dtype == 1;
+  p.dump_stride = a->dump_kv_stride;
+  p.dump_heads = a->dump_num_heads;
+  p.dump_flags = a->dump_mode_flags;
+  p.page_scores = a->page_scores;
+  p.ps_stride = a->page_score_stride;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((layout->num_waves + 3) / 4);
+  for (int c = 0; c < 3; ++c) {
+    if (!(a->class_mask & (1 << c))) continue;
+    p.indptr_off = off.indptr[c];
+    p.items_off = off.items[c];
+    if (c == 0)
+      hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, s, p);
+    else if (c == 1)
+      hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(attention_kernel<3>, grid, dim3(256), 0, s, p);
+    ASPIRE_CHECK_LAUNCH();
+  }
+  if (a->launch_merge) {
+    MergeParams mp;
+    mp.plan = p.plan;
+    mp.merge_off = off.merge;
+    mp.part_o = p.part_o;
+    mp.part_lse = p.part_lse;
+    mp.out = p.out;
+    mp.o_st = p.o_st;
+    mp.o_sh = p.o_sh;
+    mp.lse = p.lse;
+    mp.hq = p.hq;
+    mp.group = p.group;
+    const int blocks = std::min(layout->max_merge, 2048);
+    hipLaunchKernelGGL(merge_kernel, dim3(blocks), dim3(256), 0, s, mp);
+    ASPIRE_CHECK_LAUNCH();
+  }
+  return ASPIRE_OK;
+}
+
+extern "C" int aspire_merge_states(const float* v, const float* s, int32_t num_states, int64_t rows,
+                                   int32_t head_dim, void* v_out, int32_t out_dtype, float* s_out,
+                                   void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(head_dim == kHeadDim, "head_dim must be 128");
+  ASPIRE_CHECK_ARG(num_states >= 1 && rows >= 0, "bad sizes");
+  if (rows == 0) return ASPIRE_OK;
+  ASPIRE_CHECK_ARG(v && s && v_out, "null pointer");
+  ASPIRE_CHECK_ARG(al16(v) && al16(v_out), "v and v_out must be 16-byte aligned");
+  const int64_t threads = rows * 32;
+  const int64_t blocks = (threads + 255) / 256;
+  ASPIRE_CHECK_ARG(blocks < (int64_t(1) << 31), "too many rows");
+  hipLaunchKernelGGL(merge_states_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), v, s, num_states, rows, v_out,
+                     out_dtype == 1 ? 1 : 0, s_out);
+  ASPIRE_CHECK_LAUNCH();
+  return ASPIRE_OK;
+}

@@ -1,0 +1,139 @@
+// Shared host/device helpers for libaspire_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/aspire_hip.h"
+
+namespace aspire {
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char* fmt, ...);
+const char* last_error();
+
+inline int fail(int code, const char* msg) {
+  set_error("%s", msg);
+  return code;
+}
+
+#define ASPIRE_CHECK_ARG(cond, msg)                         \
+  do {                                                      \
+    if (!(cond)) {                                          \
+      ::aspire::set_error("%s: %s", __func__, msg);         \
+      return ASPIRE_ERR_INVALID;                            \
+    }                                                       \
+  } while (0)
+
+#define ASPIRE_CHECK_HIP(expr)                                                   \
+  do {                                                                           \
+    hipError_t _e = (expr);                                                      \
+    if (_e != hipSuccess) {                                                      \
+      ::aspire::set_error("%s: %s failed: %s", __func__, #expr, hipGetErrorString(_e)); \
+      return ASPIRE_ERR_HIP;                                                     \
+    }                                                                            \
+  } while (0)
+
+#define ASPIRE_CHECK_LAUNCH()                                                    \
+  do {                                                                           \
+    hipError_t _e = hipGetLastError();                                           \
+    if (_e != hipSuccess) {                                                      \
+      ::aspire::set_error("%s: kernel launch failed: %s", __func__, hipGetErrorString(_e)); \
+      return ASPIRE_ERR_HIP;                                                     \
+    }                                                                            \
+  } while (0)
+
+// ------------------------------------------------------------ constants --
+constexpr int kHeadDim = 128;
+constexpr int kPage = 16;
+constexpr int kMaxRowTiles = 3;  // q_len * group <= 48
+
+// Work item of the attention plan (8 x int32, read with scalar loads).
+struct WorkItem {
+  int32_t q_start;      // first token of the row in q / out
+  int32_t q_len;        // tokens of the row
+  int32_t kv_len;       // tokens in the row's (or segment's) page list
+  int32_t list_base;    // kv_indices offset where the list starts
+  int32_t page_begin;   // page range [page_begin, page_end) of this piece
+  int32_t page_end;
+  int32_t bg;           // (row << 8) | kv_head
+  int32_t partial_row;  // first fp32 partial row, or -1 for a final write
+};
+
+// A split (row, kv head) segment whose pieces are merged (8 x int32).
+struct MergeItem {
+  int32_t q_start;
+  int32_t q_len;
+  int32_t bg;
+  int32_t first_partial_row;
+  int32_t num_pieces;
+  int32_t rows;         // q_len * group; partials of piece i start at first + i*rows
+  int32_t pad0;
+  int32_t pad1;
+};
+
+// Fixed offsets (int32 units) of the plan in the int workspace.
+struct PlanOffsets {
+  int64_t header;        // [0]=items c0, [1]=c1, [2]=c2, [3]=num_merge
+  int64_t indptr[3];     // num_waves + 1 entries each
+  int64_t items[3];      // max_items WorkItems each
+  int64_t merge;         // max_merge MergeItems
+  int64_t total;         // int32 count
+};
+
+inline PlanOffsets plan_offsets(const aspire_plan_layout& L) {
+  PlanOffsets o;
+  o.header = 0;
+  int64_t cur = 32;
+  for (int c = 0; c < 3; ++c) {
+    o.indptr[c] = cur;
+    cur += L.num_waves + 1;
+  }
+  cur = (cur + 7) & ~int64_t(7);
+  for (int c = 0; c < 3; ++c) {
+    o.items[c] = cur;
+    cur += int64_t(L.max_items) * 8;
+  }
+  o.merge = cur;
+  cur += int64_t(L.max_merge) * 8;
+  o.total = cur;
+  return o;
+}
+
+// ------------------------------------------------------- device helpers --
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+__device__ __forceinline__ f32x4 mfma_16x16x32_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x16_bf16(i16x4 a, i16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// fp32 -> bf16 with round-to-nearest-even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  return bf16_rne_bits(lo) | (bf16_rne_bits(hi) << 16);
+}
+// fp32 values that are exactly representable in bf16: keep the upper halves.
+__device__ __forceinline__ uint32_t pack_bf16x2_exact(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+}  // namespace aspire

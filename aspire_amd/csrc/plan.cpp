@@ -1,0 +1,271 @@
+// (a7) Host planner for the mixed attention kernel.
+//
+// The attention kernel is persistent: each row-tile class (<=16, <=32, <=48
+// query rows per (row, kv head) segment) runs a fixed grid of `num_waves`
+// waves, and wave w processes the work items items[indptr[w] .. indptr[w+1]).
+// The plan lives at fixed offsets of the device int workspace, so a run()
+// captured in a HIP graph replays correctly after any later plan.
+//
+// Decomposition (stream-K): the segments of a class are laid end to end as a
+// sequence of page-heads (one page of one kv head = 16 tokens x 2 x 256 B);
+// wave w takes the contiguous range [w*T/W, (w+1)*T/W). A segment cut by a
+// range boundary is split into pieces that write fp32 partial (o, lse) rows;
+// a merge item per split segment combines them. This balances HBM traffic
+// per wave exactly and creates at most two split pieces per wave, unlike a
+// fixed chunk length.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+
+namespace aspire {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kMinPagesPerWave = 8;
+
+struct Segment {
+  int32_t q_start, q_len, kv_len, list_base, npages, bg, rows;
+};
+
+struct Scratch {
+  std::vector<Segment> segs[3];
+  std::vector<std::pair<int32_t, WorkItem>> items;
+  std::vector<MergeItem> merges;
+  std::vector<int32_t> counts;
+};
+
+int cached_cu_count() {
+  static thread_local int dev_cached = -1;
+  static thread_local int cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (dev != dev_cached) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return -1;
+    dev_cached = dev;
+  }
+  return cus;
+}
+
+}  // namespace
+}  // namespace aspire
+
+extern "C" int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu, int64_t int_ws_bytes,
+                                       int64_t float_ws_bytes, int32_t head_dim,
+                                       aspire_plan_layout* out) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(out != nullptr, "null layout");
+  ASPIRE_CHECK_ARG(head_dim == kHeadDim, "head_dim must be 128");
+  if (num_cus <= 0) {
+    num_cus = cached_cu_count();
+    if (num_cus <= 0) return fail(ASPIRE_ERR_HIP, "aspire_plan_layout_init: cannot query CU count");
+  }
+  if (waves_per_cu <= 0) waves_per_cu = 8;
+  int32_t waves = num_cus * waves_per_cu;
+  waves = (waves + kWavesPerBlock - 1) / kWavesPerBlock * kWavesPerBlock;
+  aspire_plan_layout L;
+  L.num_waves = waves;
+  L.max_items = 4 * waves + 8192;
+  L.max_merge = 2 * waves + 8192;
+  L.head_dim = head_dim;
+  PlanOffsets o = plan_offsets(L);
+  while (o.total * 4 > int_ws_bytes && L.max_items > waves + 64) {
+    L.max_items = (L.max_items + waves) / 2;
+    L.max_merge = (L.max_merge + waves) / 2;
+    o = plan_offsets(L);
+  }
+  if (o.total * 4 > int_ws_bytes)
+    return fail(ASPIRE_ERR_CAPACITY, "aspire_plan_layout_init: int workspace too small");
+  L.int_ws_bytes = o.total * 4;
+  L.partial_rows_cap = float_ws_bytes / (int64_t(head_dim + 1) * 4);
+  L.float_ws_bytes = L.partial_rows_cap * (head_dim + 1) * 4;
+  if (L.partial_rows_cap <= 0)
+    return fail(ASPIRE_ERR_CAPACITY, "aspire_plan_layout_init: float workspace too small");
+  *out = L;
+  return ASPIRE_OK;
+}
+
+extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t* qo_indptr,
+                                 const int32_t* kv_indptr, const int32_t* kv_len, int32_t batch,
+                                 int32_t per_head_lists, int32_t num_qo_heads,
+                                 int32_t num_kv_heads, int32_t page_size, int32_t causal,
+                                 void* host_buf, int64_t host_buf_bytes, aspire_plan_info* info) {
+  using namespace aspire;
+  (void)causal;  // the last query of a row sees every key, so the range is causal-independent
+  ASPIRE_CHECK_ARG(layout && host_buf && info, "null argument");
+  ASPIRE_CHECK_ARG(batch >= 0, "negative batch");
+  ASPIRE_CHECK_ARG(batch == 0 || (qo_indptr && kv_indptr && kv_len), "null plan array");
+  ASPIRE_CHECK_ARG(page_size == kPage, "page_size must be 16");
+  ASPIRE_CHECK_ARG(num_kv_heads > 0 && num_kv_heads < 256, "num_kv_heads must be in [1, 255]");
+  ASPIRE_CHECK_ARG(num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,
+                   "num_qo_heads must be a multiple of num_kv_heads");
+  ASPIRE_CHECK_ARG(batch < (1 << 23), "batch too large");
+  const aspire_plan_layout& L = *layout;
+  const PlanOffsets off = plan_offsets(L);
+  ASPIRE_CHECK_ARG(host_buf_bytes >= off.total * 4, "host plan buffer smaller than the layout");
+  const int group = num_qo_heads / num_kv_heads;
+  const int W = L.num_waves;
+
+  static thread_local Scratch sc;
+  for (auto& s : sc.segs) s.clear();
+  sc.items.clear();
+  sc.merges.clear();
+
+  int max_rows = 0;
+  int num_segments = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int q_len = qo_indptr[b + 1] - qo_indptr[b];
+    if (q_len <= 0) continue;
+    const int rows = q_len * group;
+    if (rows > 16 * kMaxRowTiles) {
+      set_error("aspire_plan_build: row %d has q_len %d; q_len * group must be <= %d", b, q_len,
+                16 * kMaxRowTiles);
+      return ASPIRE_ERR_INVALID;
+    }
+    max_rows = std::max(max_rows, rows);
+    const int cls = (rows - 1) / 16;
+    for (int g = 0; g < num_kv_heads; ++g) {
+      const int s = per_head_lists ? b * num_kv_heads + g : b;
+      const int kvl = kv_len[s];
+      const int list_pages = kv_indptr[s + 1] - kv_indptr[s];
+      if (kvl < 0 || list_pages < 0) {
+        set_error("aspire_plan_build: segment %d has negative length", s);
+        return ASPIRE_ERR_INVALID;
+      }
+      const int np = (kvl + kPage - 1) / kPage;
+      if (np > list_pages) {
+        set_error("aspire_plan_build: segment %d needs %d pages but its list holds %d", s, np,
+                  list_pages);
+        return ASPIRE_ERR_INVALID;
+      }
+      sc.segs[cls].push_back(
+          Segment{qo_indptr[b], q_len, kvl, kv_indptr[s], np, (b << 8) | g, rows});
+      ++num_segments;
+      if (!per_head_lists && g == 0) {
+        // the row-shared list is the same for every kv head; nothing more to check
+      }
+    }
+  }
+
+  int32_t* buf = static_cast<int32_t*>(host_buf);
+  int64_t partial_rows = 0;
+  int64_t total_pages = 0;
+  int num_items[3] = {0, 0, 0};
+
+  for (int c = 0; c < 3; ++c) {
+    const auto& segs = sc.segs[c];
+    int64_t T = 0;
+    for (const auto& s : segs) T += s.npages;
+    total_pages += T;
+    // Waves actually used: enough that each streams >= kMinPagesPerWave pages.
+    int64_t w_eff = std::max<int64_t>(1, std::min<int64_t>(W, T / kMinPagesPerWave));
+    // Shrink until the split pieces' partial rows fit the float workspace.
+    for (;;) {
+      sc.items.clear();
+      int64_t pr = partial_rows;
+      size_t merges_before = sc.merges.size();
+      int64_t seg_off = 0;
+      int zero_rr = 0;
+      for (const auto& s : segs) {
+        if (s.npages == 0) {
+          WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, 0, 0, s.bg, -1};
+          sc.items.emplace_back(static_cast<int32_t>(zero_rr++ % w_eff), it);
+          continue;
+        }
+        const int64_t a = seg_off, e = seg_off + s.npages;
+        // wave containing global page a: largest w with floor(w*T/w_eff) <= a
+        int64_t w_lo = (a * w_eff) / T;
+        while (w_lo > 0 && (w_lo * T) / w_eff > a) --w_lo;
+        while (w_lo + 1 < w_eff && ((w_lo + 1) * T) / w_eff <= a) ++w_lo;
+        int64_t w_hi = ((e - 1) * w_eff) / T;
+        while (w_hi > 0 && (w_hi * T) / w_eff > e - 1) --w_hi;
+        while (w_hi + 1 < w_eff && ((w_hi + 1) * T) / w_eff <= e - 1) ++w_hi;
+        const int pieces = static_cast<int>(w_hi - w_lo + 1);
+        const int first_row = pieces > 1 ? static_cast<int>(pr) : -1;
+        for (int64_t w = w_lo; w <= w_hi; ++w) {
+          const int64_t wb = std::max(a, (w * T) / w_eff);
+          const int64_t we = std::min(e, ((w + 1) * T) / w_eff);
+          WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, static_cast<int32_t>(wb - a),
+                      static_cast<int32_t>(we - a), s.bg,
+                      pieces > 1 ? static_cast<int32_t>(pr) : -1};
+          if (pieces > 1) pr += s.rows;
+          sc.items.emplace_back(static_cast<int32_t>(w), it);
+        }
+        if (pieces > 1)
+          sc.merges.push_back(MergeItem{s.q_start, s.q_len, s.bg, first_row, pieces, s.rows, 0, 0});
+        seg_off = e;
+      }
+      if (pr <= L.partial_rows_cap || w_eff == 1) {
+        if (pr > L.partial_rows_cap)
+          return fail(ASPIRE_ERR_CAPACITY, "aspire_plan_build: float workspace too small");
+        partial_rows = pr;
+        break;
+      }
+      sc.merges.resize(merges_before);
+      w_eff = std::max<int64_t>(1, w_eff / 2);
+    }
+    if (static_cast<int64_t>(sc.items.size()) > L.max_items) {
+      set_error("aspire_plan_build: class %d needs %zu work items, capacity %d", c,
+                sc.items.size(), L.max_items);
+      return ASPIRE_ERR_CAPACITY;
+    }
+    // CSR by wave (stable: keeps each wave's pieces in page order).
+    sc.counts.assign(W + 1, 0);
+    for (const auto& pi : sc.items) sc.counts[pi.first + 1]++;
+    for (int w = 0; w < W; ++w) sc.counts[w + 1] += sc.counts[w];
+    int32_t* indptr = buf + off.indptr[c];
+    std::memcpy(indptr, sc.counts.data(), sizeof(int32_t) * (W + 1));
+    WorkItem* items = reinterpret_cast<WorkItem*>(buf + off.items[c]);
+    for (const auto& pi : sc.items) items[sc.counts[pi.first]++] = pi.second;
+    num_items[c] = static_cast<int>(sc.items.size());
+  }
+  if (static_cast<int64_t>(sc.merges.size()) > L.max_merge) {
+    set_error("aspire_plan_build: %zu merge items, capacity %d", sc.merges.size(), L.max_merge);
+    return ASPIRE_ERR_CAPACITY;
+  }
+  if (!sc.merges.empty())
+    std::memcpy(buf + off.merge, sc.merges.data(), sizeof(MergeItem) * sc.merges.size());
+  std::memset(buf + off.header, 0, 32 * sizeof(int32_t));
+  buf[off.header + 0] = num_items[0];
+  buf[off.header + 1] = num_items[1];
+  buf[off.header + 2] = num_items[2];
+  buf[off.header + 3] = static_cast<int32_t>(sc.merges.size());
+
+  info->num_items[0] = num_items[0];
+  info->num_items[1] = num_items[1];
+  info->num_items[2] = num_items[2];
+  info->num_merge = static_cast<int32_t>(sc.merges.size());
+  info->partial_rows = partial_rows;
+  info->num_segments = num_segments;
+  info->max_rows = max_rows;
+  info->total_pages = total_pages;
+  info->live_bytes = (off.items[0] + int64_t(num_items[0] + num_items[1] + num_items[2]) * 8 +
+                      int64_t(sc.merges.size()) * 8) *
+                     4;
+  return ASPIRE_OK;
+}
+
+extern "C" int aspire_plan_upload(const aspire_plan_layout* layout, const aspire_plan_info* info,
+                                  const void* host_buf, void* dev_buf, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(layout && info && host_buf && dev_buf, "null argument");
+  const PlanOffsets off = plan_offsets(*layout);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const char* h = static_cast<const char*>(host_buf);
+  char* d = static_cast<char*>(dev_buf);
+  // Header and the three indptr arrays are contiguous.
+  ASPIRE_CHECK_HIP(hipMemcpyAsync(d, h, off.items[0] * 4, hipMemcpyHostToDevice, s));
+  for (int c = 0; c < 3; ++c) {
+    const int64_t n = int64_t(info->num_items[c]) * 8 * 4;
+    if (n > 0)
+      ASPIRE_CHECK_HIP(hipMemcpyAsync(d + off.items[c] * 4, h + off.items[c] * 4, n,
+                                      hipMemcpyHostToDevice, s));
+  }
+  const int64_t nm = int64_t(info->num_merge) * 8 * 4;
+  if (nm > 0)
+    ASPIRE_CHECK_HIP(
+        hipMemcpyAsync(d + off.merge * 4, h + off.merge * 4, nm, hipMemcpyHostToDevice, s));
+  return ASPIRE_OK;
+}

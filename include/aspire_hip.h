@@ -1,0 +1,233 @@
+/*
+ * aspire_hip.h - C ABI of the MI355X (gfx950) mixed draft/verify paged-KV
+ * attention library (libaspire_hip.so).
+ *
+ * Plain pointers, sizes and strides only. Every device entry point takes the
+ * HIP stream to enqueue on (a hipStream_t passed as void*; NULL = the null
+ * stream), never synchronises, and returns 0 on success or a nonzero
+ * aspire_status code; aspire_last_error() then describes the failure (the
+ * message is per host thread).
+ *
+ * Tensor conventions (all element strides, not bytes):
+ *   q / out      [T, H_q, 128] bf16, head_dim contiguous
+ *   kv_cache     [P, 2, 16, H_kv, 128] bf16: K at [:,0], V at [:,1]
+ *   page lists   int32 CSR: kv_indptr (pages) + kv_indices (physical page ids)
+ *   lse          [T, H_q] fp32, base-2 log-sum-exp
+ */
+#ifndef ASPIRE_HIP_H
+#define ASPIRE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum aspire_status {
+  ASPIRE_OK = 0,
+  ASPIRE_ERR_INVALID = 1,     /* bad argument, shape or unsupported configuration */
+  ASPIRE_ERR_CAPACITY = 2,    /* a workspace or plan capacity would be exceeded */
+  ASPIRE_ERR_HIP = 3          /* a HIP runtime call failed */
+};
+
+/* Description of the last failure on this host thread ("" if none). */
+const char* aspire_last_error(void);
+
+/* Build identity: version, target and compile flags.
+ * Replaces validate_flashinfer_patch (aspire/attention/flashinfer.py:14-60),
+ * which checked the patched FlashInfer sources; the Python layer returns this
+ * string and its sha256 in the same dict shape. */
+const char* aspire_build_info(void);
+
+/* KV tile (tokens) the attention kernel processes per step, the pad multiple
+ * for the logits-dump stride. Replaces compute_max_cta_tile_kv
+ * (aspire/attention/flashinfer.py:63-105). The kernel keeps the kv_idx < kv_len
+ * guard on dump writes, so any stride >= max_seq_length is safe. */
+int32_t aspire_max_kv_tile(void);
+
+/* ---------------------------------------------------------------- (a1) -- */
+/* Paged KV append. Replaces mylib::update_kv_padded
+ * (aspire/attention/kv_ops.py:127-187) and its three launches: FlashInfer
+ * get_seq_lens (kv_ops.py:141-143), get_batch_indices_positions_kernel
+ * (kv_ops.py:144-156) and _append_paged_kv_cache_padded_kernel
+ * (kv_ops.py:63-124), fused into one kernel.
+ * Row b of the first num_seq rows (num_seq = len(kv_last_page_len)) owns the
+ * append tokens [append_indptr[b], append_indptr[b+1]) and the pages
+ * kv_page_indices[kv_page_indptr[b] : kv_page_indptr[b+1]];
+ * append_indptr and kv_page_indptr hold at least num_seq + 1 entries.
+ * Token i of row b lands at position kv_len_b - (append_indptr[b+1] - i) with
+ * kv_len_b = max(pages_b - 1, 0) * page_size + kv_last_page_len[b]; tokens
+ * with a negative position, of rows without pages, past kv_len_b, or covered
+ * by no row are skipped. head_dim must be 128; k and v rows must be
+ * contiguous per head (the reference raises ValueError otherwise). */
+int aspire_paged_kv_append(const void* k, const void* v,
+                           int64_t k_stride_n, int64_t k_stride_h,
+                           int64_t v_stride_n, int64_t v_stride_h,
+                           const int32_t* append_indptr,
+                           const int32_t* kv_page_indices,
+                           const int32_t* kv_page_indptr,
+                           const int32_t* kv_last_page_len, int32_t num_seq,
+                           void* kv_cache, int64_t cache_stride_p,
+                           int64_t cache_stride_kv, int64_t cache_stride_t,
+                           int64_t cache_stride_h, int32_t total_tokens,
+                           int32_t num_heads, int32_t head_dim,
+                           int32_t page_size, void* stream);
+
+/* ---------------------------------------------------------------- (a2) -- */
+/* Mixed draft/verify page list. Replaces build_unified_indices and
+ * _copy_indices_kernel (aspire/models/sparse_draft_runner.py:92-153):
+ * n_b = mode_flags[b] == 0 (DRAFT) ? draft_num_pages[b] : verify_num_pages[b];
+ * indptr[0] = 0, indptr[b+1] = sum_{c<=b} n_c; the n_b entries read from the
+ * flattened source table at b * width (draft or verify) are copied to
+ * indices[indptr[b]]. When indptr_fill_to > batch + 1, entries
+ * indptr[batch+1 : indptr_fill_to] are set to indptr[batch] (the padding-row
+ * fill of aspire/backends/base.py:1253-1255). mode_flags_elem_size is 1, 4
+ * or 8 (bool/uint8, int32, int64). Reads are bounded by draft_rows * width
+ * and verify_rows * width; writes by indices_capacity (exceeding it sets no
+ * error on the device: those entries are dropped). */
+int aspire_build_mixed_page_list(const void* mode_flags, int32_t mode_flags_elem_size,
+                                 const int32_t* draft_indices, int64_t draft_width,
+                                 int64_t draft_rows,
+                                 const int32_t* verify_indices, int64_t verify_width,
+                                 int64_t verify_rows,
+                                 const int32_t* draft_num_pages,
+                                 const int32_t* verify_num_pages, int32_t batch,
+                                 int32_t* paged_kv_indices, int64_t indices_capacity,
+                                 int32_t* paged_kv_indptr, int32_t indptr_fill_to,
+                                 void* stream);
+
+/* ---------------------------------------------------------------- (a7) -- */
+/* Work plan for the mixed attention kernel. Replaces the patched FlashInfer
+ * TwoStageHolisticPlan (third_party/flashinfer/aspire.patch:108-288) behind
+ * HolisticAttentionWrapper.plan / plan_host
+ * (aspire/attention/holistic_wrapper.py:200-342).
+ * The plan lives at fixed offsets of a device int workspace (so a captured
+ * run() replays with new plans); aspire_plan_build fills a host (pinned)
+ * mirror with no HIP calls and aspire_plan_upload copies its live segments
+ * asynchronously on the given stream. */
+typedef struct aspire_plan_layout {
+  int32_t num_waves;          /* persistent waves per row-tile class kernel */
+  int32_t max_items;          /* work items per class */
+  int32_t max_merge;          /* split segments needing a merge */
+  int32_t head_dim;           /* 128 */
+  int64_t partial_rows_cap;   /* fp32 partial rows (head_dim + 1 floats each) */
+  int64_t int_ws_bytes;       /* bytes of the int workspace the layout uses */
+  int64_t float_ws_bytes;     /* bytes of the float workspace the layout uses */
+} aspire_plan_layout;
+
+typedef struct aspire_plan_info {
+  int32_t num_items[3];       /* per row-tile class (<=16, <=32, <=48 rows) */
+  int32_t num_merge;
+  int64_t partial_rows;
+  int32_t num_segments;       /* (row, kv head) segments with queries */
+  int32_t max_rows;           /* largest q_len * group of any segment */
+  int64_t total_pages;        /* page-heads the plan streams */
+  int64_t live_bytes;         /* bytes the upload copies */
+} aspire_plan_info;
+
+/* num_cus <= 0 queries the current device. waves_per_cu <= 0 uses 8. */
+int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu,
+                            int64_t int_ws_bytes, int64_t float_ws_bytes,
+                            int32_t head_dim, aspire_plan_layout* out);
+
+/* Rows b in [0, batch) have queries [qo_indptr[b], qo_indptr[b+1]) (host
+ * arrays). per_head_lists == 0: kv_indptr has batch+1 entries and kv_len batch
+ * entries (one page list per row, shared by its kv heads); otherwise
+ * batch*num_kv_heads+1 and batch*num_kv_heads, one list per (row, kv head),
+ * segment index b*num_kv_heads + g. q_len * (num_qo_heads / num_kv_heads)
+ * must be <= 48. */
+int aspire_plan_build(const aspire_plan_layout* layout, const int32_t* qo_indptr,
+                      const int32_t* kv_indptr, const int32_t* kv_len, int32_t batch,
+                      int32_t per_head_lists, int32_t num_qo_heads,
+                      int32_t num_kv_heads, int32_t page_size, int32_t causal,
+                      void* host_buf, int64_t host_buf_bytes,
+                      aspire_plan_info* info);
+
+int aspire_plan_upload(const aspire_plan_layout* layout, const aspire_plan_info* info,
+                       const void* host_buf, void* dev_buf, void* stream);
+
+/* ------------------------------------------------------- (a4, a5, a6) -- */
+/* Mixed draft/verify attention over a plan. Replaces
+ * HolisticAttentionWrapper.run (aspire/attention/holistic_wrapper.py:344-386)
+ * and the patched BatchPagedAttentionPersistent<64,16,...> kernel it runs
+ * (aspire.patch:18-21), including the split-KV merge (aspire.patch:81-85,
+ * 257-273) and, when dump_kind != 0, the logits-dump variant bound at the
+ * refresh layer (aspire/backends/base.py:452-514, jit_kernels.py:74-96,
+ * 182-193, 247-256). page_scores != NULL adds the per-KV-head key-mean page
+ * score of BASELINE config 2 (no reference counterpart). */
+typedef struct aspire_attention_args {
+  const void* q; int64_t q_stride_t; int64_t q_stride_h;
+  const void* kv_cache; int64_t cache_stride_p; int64_t cache_stride_kv;
+  int64_t cache_stride_t; int64_t cache_stride_h;
+  const int32_t* kv_indices;
+  void* out; int64_t out_stride_t; int64_t out_stride_h;
+  float* lse;                     /* [T, H_q] contiguous, or NULL */
+  const void* plan_dev;           /* device int workspace holding the plan */
+  float* float_ws;                /* device float workspace (partials) */
+  int32_t num_qo_heads; int32_t num_kv_heads; int32_t head_dim; int32_t page_size;
+  float sm_scale; int32_t causal;
+  int32_t class_mask;             /* bit c launches row-tile class c; 7 = all (graph-safe) */
+  int32_t launch_merge;           /* 0 skips the merge launch (no split segment) */
+  /* logits dump: kind 0 none, 1 last_token (1 slot), 2 first_last (2 slots) */
+  void* dump; int32_t dump_kind; int32_t dump_dtype; /* 0 fp16, 1 fp32 */
+  int64_t dump_kv_stride; int32_t dump_num_heads;
+  const int32_t* dump_mode_flags; /* per row, 0 disables; NULL = all rows */
+  float* page_scores; int64_t page_score_stride; /* [segments, stride] or NULL */
+} aspire_attention_args;
+
+int aspire_attention_run(const aspire_plan_layout* layout,
+                         const aspire_attention_args* args, void* stream);
+
+/* ---------------------------------------------------------------- (a6) -- */
+/* Standalone merge of num_states partial states (FlashInfer merge_states
+ * semantics, base-2 lse): v [num_states, rows, head_dim] fp32, s
+ * [num_states, rows] fp32 -> v_out [rows, head_dim] (out_dtype 0 fp32,
+ * 1 bf16), s_out [rows]. */
+int aspire_merge_states(const float* v, const float* s, int32_t num_states,
+                        int64_t rows, int32_t head_dim, void* v_out,
+                        int32_t out_dtype, float* s_out, void* stream);
+
+/* ---------------------------------------------------------------- (a3) -- */
+/* Reference page scoring (R). slots == 2 replaces
+ * PageSelectorFirstLastAvg.select / select_subset
+ * (aspire/backends/page_selector.py:206-233) and _select_first_last_impl
+ * (163-181); slots == 1 replaces PageSelector.select / select_subset (140-157)
+ * and _select_impl (110-130). Page score j of row r (row_ids[r] or r):
+ *   sum_{t in page j, t < max_seq_length} sum_{slot} max_h
+ *     exp2(nan_to_num(fp32(fp16(dump * sm_scale_log2e)) - lse[q_slot, h]))
+ *   + (-j * 1e-7f)
+ * where q_slot is the row's first query (slot 0 of 2) or last query, for
+ * j < num_pages[row], written to scores[r * score_stride + j]. The dump is
+ * fp16 [bsz, n_heads, slots, kv_stride]. */
+int aspire_select_first_last_scores(const void* dump, int64_t kv_stride, int32_t n_heads,
+                                    int32_t bsz, int32_t max_seq_length,
+                                    const float* lse, int32_t lse_rows,
+                                    const int32_t* qo_indptr, const int32_t* num_pages,
+                                    const int32_t* row_ids, int32_t rows,
+                                    int32_t page_size, float sm_scale_log2e,
+                                    float* scores, int64_t score_stride, int32_t slots,
+                                    void* stream);
+
+/* Top-k page selection for rows (R) or (row, kv head) segments (B).
+ * Replaces _finalize_scores (page_selector.py:79-108) and
+ * compute_valid_counts (52-62). For segment s (table row = row_ids[s /
+ * segs_per_row] or s / segs_per_row): pages j < n = num_pages[that row] with
+ * j >= n - L forced in; k_s = valid count (count_mode 0: min(n, subset);
+ * 1: min(n, min_pages); 2: clamp(ceil(fp32(n) * pct / 100), min(n,
+ * min_pages), min(n, subset))); the k_s best pages are looked up in the
+ * table and written to selected[s * sel_stride + 0 .. k_s) in ascending
+ * physical (order 0, the reference rule) or logical (order 1) page order,
+ * zeros up to sel_width; valid[s] = k_s (if valid != NULL). */
+int aspire_select_topk(const float* scores, int64_t score_stride, const int32_t* num_pages,
+                       const int32_t* row_ids, int32_t segments, int32_t segs_per_row,
+                       int32_t L, int32_t count_mode, int32_t subset, int32_t min_pages,
+                       float pct, const int32_t* block_table, int64_t table_stride,
+                       int32_t order, int32_t* selected, int64_t sel_stride,
+                       int32_t sel_width, int32_t* valid, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASPIRE_HIP_H */

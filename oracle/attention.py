@@ -109,7 +109,7 @@ def paged_attention(
         lse = torch.zeros((T, hq), dtype=torch.float32)
     qf = q.to(compute_dtype)
     for b in range(bsz):
-        q0, q1 = qo[b], qo[b + 1]
+        q0, q1 = qo[b], min(qo[b + 1], T)
         qlen = q1 - q0
         if qlen <= 0:
             continue

@@ -1,0 +1,162 @@
+"""Split-KV merge and page selection on the GPU."""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from aspire_amd import _lib
+from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
+from aspire_amd.backends.page_selector import KeyMeanPageSelector, PageSelector, PageSelectorFirstLastAvg
+from aspire_amd.workloads import PAGE, build_step
+from helpers import assert_topk_sets, say
+from oracle.attention import paged_attention
+from oracle.merge import merge_states
+from oracle.select import FirstLastSelector, topk_pages_per_head
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden" / "select_first_last.npz"
+
+
+@pytest.mark.parametrize("n", [1, 2, 5])
+def test_merge_states_matches_oracle(gpu, n):
+    say("merge_states", n)
+    g = torch.Generator().manual_seed(n)
+    rows = 333
+    v = torch.randn(n, rows, 128, generator=g)
+    s = torch.randn(n, rows, generator=g) * 4
+    if n > 1:
+        s[1, :7] = float("-inf")
+    ref_o, ref_s = merge_states(v, s)
+    vd, sd = v.to(gpu), s.to(gpu)
+    o32 = torch.empty(rows, 128, device=gpu)
+    o16 = torch.empty(rows, 128, device=gpu, dtype=torch.bfloat16)
+    so = torch.empty(rows, device=gpu)
+    L = _lib.lib()
+    st = _lib.stream_of(vd)
+    _lib.check(L.aspire_merge_states(_lib.ptr(vd), _lib.ptr(sd), n, rows, 128, _lib.ptr(o32), 0, _lib.ptr(so), st), "m")
+    _lib.check(L.aspire_merge_states(_lib.ptr(vd), _lib.ptr(sd), n, rows, 128, _lib.ptr(o16), 1, None, st), "m")
+    torch.cuda.synchronize()
+    assert torch.allclose(o32.cpu(), ref_o, atol=1e-5, rtol=1e-5)
+    assert torch.allclose(so.cpu(), ref_s, atol=1e-5)
+    assert torch.allclose(o16.float().cpu(), ref_o, atol=2e-2)
+
+
+def _golden_case(z, name, gpu, order):
+    g = lambda k: z[f"{name}/{k}"]
+    B, H, page, max_seq, kv_stride, subset, L, pct, min_pages = g("params").tolist()
+    kw = dict(max_batch_size=int(B), pages_per_slot=int(max_seq) // int(page), subset_cache_size=int(subset), L=int(L),
+              n_heads=int(H), page_size=int(page), max_seq_length=int(max_seq), device=gpu, bsz=int(B), dec_len=8,
+              head_dim=128, kv_stride=int(kv_stride), draft_percent=None if pct < 0 else float(pct),
+              min_draft_pages=int(min_pages))
+    sel = PageSelectorFirstLastAvg(**kw, order=order)
+    dev = lambda a: torch.from_numpy(a).to(gpu)
+    inp = dict(attention_weights_buffer=dev(g("dump")).view(torch.float16), lse_buffer=dev(g("lse")),
+               num_pages=dev(g("num_pages")), block_table=dev(g("block_table")), qo_indptr=dev(g("qo_indptr")))
+    return sel, inp, g
+
+
+@pytest.mark.parametrize("name", ["small_fixed", "percent", "ties_inf"])
+def test_first_last_selector_against_reference_golden(gpu, name):
+    say("selector golden", name)
+    z = np.load(GOLDEN)
+    sel, inp, g = _golden_case(z, name, gpu, "physical")
+    selected, valid = sel.select(**inp)
+    torch.cuda.synchronize()
+    assert np.array_equal(valid.cpu().numpy(), g("valid"))
+    ref_scores = g("scores")
+    npg = g("num_pages")
+    table = g("block_table")
+    got_scores = sel._scores.cpu().numpy()
+    for b in range(len(npg)):
+        n = int(npg[b])
+        a, r = got_scores[b, :n], ref_scores[b, :n]
+        fin = np.isfinite(r)
+        assert np.array_equal(np.isfinite(a), fin)
+        assert np.allclose(a[fin], r[fin], rtol=1e-5, atol=1e-6)
+        # sets: exact wherever the gap exceeds 1e-3 (forced last-L pages are +inf)
+        eff = r.astype(np.float64).copy()
+        eff[max(n - int(sel.L), 0) : n] = np.inf
+        k = int(g("valid")[b])
+        inv = {int(p): j for j, p in enumerate(table[b])}
+        got_logical = [inv[int(p)] for p in selected[b, :k].cpu().numpy()]
+        assert_topk_sets(got_logical, eff, k)
+        row = selected[b].cpu().numpy()
+        assert np.all(np.diff(row[:k]) > 0) and not row[k:].any()
+        if name != "ties_inf":
+            assert np.array_equal(row, g("selected")[b])
+
+
+def test_selector_logical_order_and_subset(gpu):
+    z = np.load(GOLDEN)
+    sel, inp, g = _golden_case(z, "small_fixed", gpu, "logical")
+    selected, valid = sel.select(**inp)
+    table = g("block_table")
+    for b in range(4):
+        k = int(valid[b])
+        inv = {int(p): j for j, p in enumerate(table[b])}
+        logical = [inv[int(p)] for p in selected[b, :k].cpu().numpy()]
+        assert logical == sorted(logical)
+    full = selected.clone()
+    valid = valid.clone()  # the selector returns views of its preallocated buffers (as the reference does)
+    sub, sub_valid = sel.select_subset(torch.tensor([2, 0], device=gpu), **inp)
+    torch.cuda.synchronize()
+    assert torch.equal(sub[0], full[2]) and torch.equal(sub[1], full[0])
+    assert sub_valid.tolist() == [int(valid[2]), int(valid[0])]
+
+
+def test_last_token_selector_matches_torch_chain(gpu):
+    say("last-token selector")
+    B, H, page, max_seq = 3, 8, 16, 1024
+    gen = torch.Generator().manual_seed(4)
+    dump = (torch.randn(B, H, max_seq, generator=gen) * 5).to(torch.float16)
+    dump[1, :, 600:] = float("-inf")
+    lse = torch.randn(6, H, generator=gen) + 7
+    npg = torch.tensor([64, 38, 5], dtype=torch.int32)
+    table = torch.arange(B * 64, dtype=torch.int32).view(B, 64)
+    qo = torch.tensor([0, 2, 3, 6, 6], dtype=torch.int32)
+    sel = PageSelector(B, 64, 10, 2, H, page, max_seq, gpu, B, 4, min_draft_pages=10)
+    selected, valid = sel.select(dump.view(-1).to(gpu), lse.to(gpu), npg.to(gpu), table.to(gpu), qo.to(gpu))
+    torch.cuda.synchronize()
+    # the reference's last-token chain (page_selector.py:110-130), restated with torch on the CPU
+    last = (qo[1 : B + 1].long() - 1).clamp(min=0)
+    norm = dump.float() * 0 + (dump * sel._sm_scale_log2e).float() - lse[last][:, :, None]
+    norm.nan_to_num_(nan=float("-inf"))
+    tok = torch.exp2(norm.amax(dim=1))
+    scores = tok.view(B, 64, 16).sum(-1) - torch.arange(64, dtype=torch.float32) * 1e-7
+    for b in range(B):
+        n = int(npg[b])
+        eff = scores[b, :n].double().numpy().copy()
+        eff[max(n - 2, 0) :] = np.inf
+        k = min(n, 10)
+        assert int(valid[b]) == k
+        assert_topk_sets((selected[b, :k].cpu().numpy() - b * 64).tolist(), eff, k)
+
+
+def test_keymean_selector_config2_shape(gpu):
+    say("key-mean selector")
+    step = build_step(hq=32, hkv=8, ctx_len=[8192, 9000, 12000, 8200], q_len=[1] * 4, is_draft=[0] * 4,
+                      draft_budget=0, seed=21, device=gpu)
+    w = HolisticAttentionWrapper(torch.empty(1, device=gpu), "NHD")
+    w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, 32, 8, 128, PAGE, causal=True)
+    max_pages = int(step.block_table.shape[1])
+    ks = KeyMeanPageSelector(4, 8, max_pages, k=128, L=0, device=gpu)
+    ks.page_scores.fill_(float("nan"))
+    w.run(step.q, step.cache, page_scores=ks.page_scores)
+    npg = torch.from_numpy((step.ctx_len + 15) // 16).to(torch.int32).to(gpu)
+    selected, counts = ks.select(npg, step.block_table)
+    torch.cuda.synchronize()
+    ref_scores = torch.full((4 * 8, max_pages), float("nan"))
+    paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host, step.kv_indices.cpu(),
+                    step.kv_len_host, num_kv_heads=8, page_scores=ref_scores)
+    table = step.block_table.cpu().numpy()
+    for b in range(4):
+        n = int(npg[b])
+        inv = {int(p): j for j, p in enumerate(table[b, :n])}
+        for g in range(8):
+            k = int(counts[b, g])
+            assert k == min(128, n)
+            logical = [inv[int(p)] for p in selected[b, g, :k].cpu().numpy()]
+            assert logical == sorted(logical)
+            assert_topk_sets(logical, ref_scores[b * 8 + g, :n].double().numpy(), k)

@@ -1,0 +1,174 @@
+"""Host planner invariants (pure host code in libaspire_hip.so; no GPU needed)."""
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from aspire_amd import _lib
+
+LIB = Path(_lib.LIB_PATH)
+pytestmark = pytest.mark.skipif(not LIB.exists(), reason="libaspire_hip.so not built")
+
+HEADER_INTS = 32
+
+
+def layout(num_cus=256, waves_per_cu=8, float_ws=384 << 20):
+    lay = _lib.PlanLayout()
+    rc = _lib.lib().aspire_plan_layout_init(num_cus, waves_per_cu, 8 << 20, float_ws, 128, ctypes.byref(lay))
+    _lib.check(rc, "layout")
+    return lay
+
+
+def offsets(lay):
+    W = lay.num_waves
+    cur = HEADER_INTS
+    indptr = []
+    for _ in range(3):
+        indptr.append(cur)
+        cur += W + 1
+    cur = (cur + 7) & ~7
+    items = []
+    for _ in range(3):
+        items.append(cur)
+        cur += lay.max_items * 8
+    return indptr, items, cur
+
+
+def plan(lay, qo, kvp, kvl, hq, hkv, per_head=False):
+    buf = np.zeros(8 << 18, dtype=np.int32)
+    info = _lib.PlanInfo()
+    qo = np.ascontiguousarray(qo, dtype=np.int32)
+    kvp = np.ascontiguousarray(kvp, dtype=np.int32)
+    kvl = np.ascontiguousarray(kvl, dtype=np.int32)
+    batch = len(kvl) // hkv if per_head else len(kvl)
+    rc = _lib.lib().aspire_plan_build(
+        ctypes.byref(lay), qo.ctypes.data_as(ctypes.c_void_p), kvp.ctypes.data_as(ctypes.c_void_p),
+        kvl.ctypes.data_as(ctypes.c_void_p), batch, int(per_head), hq, hkv, 16, 1,
+        buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, ctypes.byref(info))
+    _lib.check(rc, "plan")
+    return buf, info
+
+
+def decode(lay, buf, info):
+    indptr_off, items_off, merge_off = offsets(lay)
+    W = lay.num_waves
+    classes = []
+    for c in range(3):
+        ip = buf[indptr_off[c] : indptr_off[c] + W + 1]
+        it = buf[items_off[c] : items_off[c] + info.num_items[c] * 8].reshape(-1, 8)
+        classes.append((ip, it))
+    merges = buf[merge_off : merge_off + info.num_merge * 8].reshape(-1, 8)
+    return classes, merges
+
+
+def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False):
+    classes, merges = decode(lay, buf, info)
+    group = hq // hkv
+    seen = {}
+    partial_rows = set()
+    for c, (ip, it) in enumerate(classes):
+        assert ip[0] == 0 and ip[-1] == len(it) and np.all(np.diff(ip) >= 0)
+        for w in range(lay.num_waves):
+            for row in it[ip[w] : ip[w + 1]]:
+                q_start, q_len, kv_len, base, pb, pe, bg, prow = row.tolist()
+                b, g = bg >> 8, bg & 255
+                assert (q_len * group - 1) // 16 == c
+                seg = b * hkv + g if per_head else b
+                assert q_start == qo[b] and q_len == qo[b + 1] - qo[b]
+                assert kv_len == kvl[seg] and base == kvp[seg]
+                for p in range(pb, pe):
+                    key = (b, g, p)
+                    assert key not in seen, f"page {key} planned twice"
+                    seen[key] = prow
+                if prow >= 0:
+                    for r in range(q_len * group):
+                        assert prow + r not in partial_rows
+                        partial_rows.add(prow + r)
+    # every page of every segment with queries is covered exactly once
+    for b in range(len(qo) - 1 if not per_head else len(kvl) // hkv):
+        if b >= (len(kvl) // hkv if per_head else len(kvl)):
+            break
+        if qo[b + 1] - qo[b] <= 0:
+            continue
+        for g in range(hkv):
+            seg = b * hkv + g if per_head else b
+            for p in range((kvl[seg] + 15) // 16):
+                assert (b, g, p) in seen
+    # merge items reference the split pieces
+    for m in merges:
+        q_start, q_len, bg, first, pieces, rows = m[:6].tolist()
+        assert pieces >= 2 and rows == q_len * group
+        for k in range(pieces):
+            assert first + k * rows in partial_rows
+    return seen
+
+
+def test_cover_and_balance_config1_shape():
+    B, hq, hkv = 32, 32, 8
+    q_len = np.array([1] * 16 + [4] * 16)
+    kvl = np.array([128 * 16] * 16 + [32768] * 16 + [0])
+    pages = (kvl + 15) // 16
+    qo = np.concatenate([[0], np.cumsum(q_len), [80]])
+    kvp = np.concatenate([[0], np.cumsum(pages[:B]), [pages[:B].sum()]])
+    lay = layout()
+    buf, info = plan(lay, qo, kvp, kvl, hq, hkv)
+    check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv)
+    assert info.total_pages == int(pages[:B].sum()) * hkv
+    # stream-K balance: every wave streams floor or ceil of the mean page count
+    classes, _ = decode(lay, buf, info)
+    ip, it = classes[0]
+    per_wave = np.array([int((it[ip[w]:ip[w + 1], 5] - it[ip[w]:ip[w + 1], 4]).sum()) for w in range(lay.num_waves)])
+    mean = info.total_pages / lay.num_waves
+    assert per_wave.max() <= np.ceil(mean) and per_wave.min() >= np.floor(mean)
+
+
+def test_mixed_classes_ragged_and_empty_rows():
+    hq, hkv = 32, 8
+    q_len = np.array([1, 2, 5, 9, 0, 3, 12 // 4 * 4 // 4, 1])
+    kvl = np.array([37, 0, 4096 + 5, 100000, 50, 17, 16, 1, 0])
+    pages = (kvl + 15) // 16
+    B = len(q_len)
+    qo = np.concatenate([[0], np.cumsum(q_len), [q_len.sum() + 3]])
+    kvp = np.concatenate([[0], np.cumsum(pages[:B]), [pages[:B].sum()]])
+    kvl_full = np.concatenate([kvl[:B], [0]])
+    lay = layout(num_cus=16, waves_per_cu=4)
+    buf, info = plan(lay, qo, kvp, kvl_full, hq, hkv)
+    check_cover(lay, buf, info, qo, kvp, kvl_full, hq, hkv)
+    assert info.num_items[2] > 0 and info.num_merge > 0
+
+
+def test_per_head_lists():
+    hq, hkv, B = 32, 8, 3
+    rng = np.random.default_rng(0)
+    kvl = rng.integers(1, 3000, size=B * hkv)
+    pages = (kvl + 15) // 16
+    kvp = np.concatenate([[0], np.cumsum(pages)])
+    qo = np.array([0, 1, 2, 3])
+    lay = layout(num_cus=8, waves_per_cu=4)
+    buf, info = plan(lay, qo, kvp, kvl, hq, hkv, per_head=True)
+    check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=True)
+
+
+def test_rejects_bad_inputs():
+    lay = layout(num_cus=4, waves_per_cu=4)
+    with pytest.raises(ValueError, match="q_len"):
+        plan(lay, np.array([0, 13]), np.array([0, 1]), np.array([16]), 32, 8)  # 13 * 4 > 48 rows
+    with pytest.raises(ValueError, match="pages"):
+        plan(lay, np.array([0, 1]), np.array([0, 1]), np.array([40]), 32, 8)  # list shorter than kv_len
+    with pytest.raises(ValueError, match="multiple"):
+        plan(lay, np.array([0, 1]), np.array([0, 1]), np.array([16]), 30, 8)
+
+
+def test_partial_capacity_shrinks_split():
+    hq, hkv = 32, 8
+    kvl = np.array([32768] * 4 + [0])
+    qo = np.array([0, 4, 8, 12, 16, 16])
+    pages = (kvl + 15) // 16
+    kvp = np.concatenate([[0], np.cumsum(pages[:4]), [pages[:4].sum()]])
+    small = layout(num_cus=64, waves_per_cu=8, float_ws=40 * 129 * 4 * 16)
+    buf, info = plan(small, qo, kvp, kvl, hq, hkv)
+    assert info.partial_rows <= small.partial_rows_cap
+    check_cover(small, buf, info, qo, kvp, kvl, hq, hkv)
