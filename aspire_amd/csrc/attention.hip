@@ -70,22 +70,53 @@ constexpr float kNegInf = -__builtin_huge_valf();
 #ifndef ASPIRE_NT1_WAVES
 #define ASPIRE_NT1_WAVES 3
 #endif
+#ifndef ASPIRE_DIM_MAP
+#define ASPIRE_DIM_MAP 1
+#endif
+#ifndef ASPIRE_NT_LOADS
+#define ASPIRE_NT_LOADS 0
+#endif
+#ifndef ASPIRE_PIPE
+#define ASPIRE_PIPE 0
+#endif
 
-__device__ __forceinline__ void load_k(const AttnParams& p, int64_t phys, int g, int r, int grp,
-                                       bool key_ok, uint4 (&dst)[4]) {
-  const uint16_t* kp = p.cache + phys * p.c_sp + int64_t(r) * p.c_st + int64_t(g) * p.c_sh + grp * 32;
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    dst[c] = key_ok ? reinterpret_cast<const uint4*>(kp)[c] : make_uint4(0, 0, 0, 0);
+// Element offset of the 8-dim slice c (0..3) a lane of group grp owns. Any
+// assignment works as long as K, V, Q and the output agree (the MFMA sums over
+// k in whatever order both operands use); with 32*c + 8*grp the four lanes of
+// one key row read 64 contiguous bytes per load instruction.
+__device__ __forceinline__ int dim_off(int grp, int c) {
+  return ASPIRE_DIM_MAP ? 32 * c + 8 * grp : 32 * grp + 8 * c;
 }
 
-__device__ __forceinline__ void load_v(const AttnParams& p, int64_t phys, int g, int r, int grp,
-                                       bool key_ok, uint4 (&dst)[4]) {
-  const uint16_t* vp =
-      p.cache + phys * p.c_sp + p.c_skv + int64_t(r) * p.c_st + int64_t(g) * p.c_sh + grp * 32;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+
+__device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
+#if ASPIRE_NT_LOADS
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *reinterpret_cast<const uint4*>(ptr);
+#endif
+}
+
+// K / V loads go through buffer resources: a per-page scalar descriptor (base =
+// the page's K or V rows of this kv head) and one per-lane 32-bit byte offset
+// that stays fixed for the whole item; slice c adds an immediate 64*c. A lane
+// whose key is past kv_len uses an offset beyond the descriptor's range, which
+// the hardware answers with zeros (no branch, no out-of-range access).
+constexpr uint32_t kBufferConfig = 0x00020000u;  // gfx9 raw buffer dword 3
+constexpr int kOutOfRange = 0x7ffffff0;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint16_t* base, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, bytes, kBufferConfig);
+}
+
+__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rsrc, int voff, uint4 (&dst)[4]) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    dst[c] = key_ok ? reinterpret_cast<const uint4*>(vp)[c] : make_uint4(0, 0, 0, 0);
+  for (int c = 0; c < 4; ++c) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + 64 * c, 0, ASPIRE_NT_LOADS ? 2 : 0);
+    dst[c] = make_uint4(v.x, v.y, v.z, v.w);
+  }
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) {
@@ -127,10 +158,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     if (row < rows) {
       const int qi = row / G;
       const int hh = row - qi * G;
-      const uint16_t* src =
-          p.q + int64_t(it.q_start + qi) * p.q_st + int64_t(g * G + hh) * p.q_sh + grp * 32;
+      const uint16_t* src = p.q + int64_t(it.q_start + qi) * p.q_st + int64_t(g * G + hh) * p.q_sh;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) qf[t][c] = as_bf16x8(reinterpret_cast<const uint4*>(src)[c]);
+      for (int c = 0; c < 4; ++c)
+        qf[t][c] = as_bf16x8(*reinterpret_cast<const uint4*>(src + dim_off(grp, c)));
       limit[t] = p.causal ? min(kv_len - it.q_len + qi, kv_len - 1) : kv_len - 1;
       row_qi[t] = qi;
     } else {
@@ -155,114 +186,169 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   const bool do_score = p.page_scores != nullptr && it.q_len == 1;
   const int dump_slots = p.dump_kind == 2 ? 2 : 1;
 
-  // Page ids are fetched 64 at a time (one per lane) and broadcast with readlane.
+  // Page ids are read with scalar loads (constant address space): they are
+  // wave-uniform, and scalar loads are tracked by lgkmcnt, so waiting for an id
+  // never drains the outstanding K/V vector loads. The id of page pg+2 is
+  // requested one iteration before use; the index is clamped into the item.
   const int pb = it.page_begin;
   const int pe = it.page_end;
-  int win_base = pb;
-  int win = (pb + lane < pe) ? p.kv_indices[it.list_base + pb + lane] : 0;
-  auto page_id = [&](int pg) -> int64_t {
-    if (pg - win_base >= 64) {
-      win_base = pg;
-      win = (pg + lane < pe) ? p.kv_indices[it.list_base + pg + lane] : 0;
-    }
-    return int64_t(__builtin_amdgcn_readlane(win, pg - win_base));
+  typedef const __attribute__((address_space(4))) int32_t* const_ids_t;
+  const const_ids_t ids = (const_ids_t)(p.kv_indices + it.list_base);
+  auto page_id = [&](int pg) -> int64_t { return int64_t(ids[min(pg, pe - 1)]); };
+
+  // Buffer-load addressing for this item: lane byte offset within one kv
+  // head's rows of a page, and the byte extent of those rows.
+  const int lane_off = (r * int(p.c_st) + 8 * grp) * 2;
+  const int rows_bytes = (15 * int(p.c_st) + kHeadDim) * 2;
+  auto load_k = [&](int64_t phys, bool ok, uint4(&dst)[4]) {
+    load_rows(page_rsrc(p.cache + phys * p.c_sp + int64_t(g) * p.c_sh, rows_bytes), ok ? lane_off : kOutOfRange,
+              dst);
+  };
+  auto load_v = [&](int64_t phys, bool ok, uint4(&dst)[4]) {
+    load_rows(page_rsrc(p.cache + phys * p.c_sp + p.c_skv + int64_t(g) * p.c_sh, rows_bytes),
+              ok ? lane_off : kOutOfRange, dst);
   };
 
-  // Single K/V register buffer, pipelined at half-page granularity: the next
+  // Per-page compute. after_qk runs once QK^T has consumed K, after_pv once
+  // P.V has consumed V (the half-page pipeline issues the next loads there).
+  auto page_body = [&](int pg, const uint4 (&kr)[4], const uint4 (&vr)[4], auto&& after_qk, auto&& after_pv) {
+      const int base_pos = pg * 16 + grp * 4;
+
+      f32x4 s[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[t] = mfma_16x16x32_bf16(as_bf16x8(kr[c]), qf[t][c], s[t]);
+      }
+      after_qk();
+
+        i16x4 pf[NT];
+      float alpha[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (do_dump && row_qi[t] >= 0) {
+          const int qi = row_qi[t];
+          int slot = -1;
+          if (p.dump_kind == 2)
+            slot = qi == 0 ? 0 : (qi == it.q_len - 1 ? 1 : -1);
+          else if (qi == it.q_len - 1)
+            slot = 0;
+          if (slot >= 0) {
+            const int head = g * G + (t * 16 + r - qi * G);
+            const int64_t base =
+                (int64_t(b * p.dump_heads + head) * dump_slots + slot) * p.dump_stride;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (base_pos + i < kv_len) store_dump(p, base + base_pos + i, s[t][i]);
+          }
+        }
+        if (do_score && t == 0) {
+          float rs = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) rs += (base_pos + i < kv_len) ? s[t][i] : 0.f;
+          rs += shfl_xor_f(rs, 16);
+          rs += shfl_xor_f(rs, 32);
+          const int cnt = min(16, kv_len - pg * 16);
+          float val = (r < G) ? rs / float(cnt) : kNegInf;
+          val = fmaxf(val, shfl_xor_f(val, 1));
+          val = fmaxf(val, shfl_xor_f(val, 2));
+          val = fmaxf(val, shfl_xor_f(val, 4));
+          val = fmaxf(val, shfl_xor_f(val, 8));
+          if (lane == 0) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + pg] = val;
+        }
+
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          x[i] = (base_pos + i <= limit[t]) ? s[t][i] * p.scale_log2 : kNegInf;
+        float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        mx = fmaxf(mx, shfl_xor_f(mx, 16));
+        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        const float m_new = fmaxf(m[t], mx);
+        float a = 1.f;
+        float pv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (m_new != kNegInf) {
+          a = __builtin_amdgcn_exp2f(m[t] - m_new);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+        }
+        l[t] = l[t] * a + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+        m[t] = m_new;
+        alpha[t] = a;
+        pf[t] = as_i16x4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]));
+      }
+
+      // O^T += V^T P^T, one 16-dim slice at a time: transpose the slice with an
+      // exact identity MFMA (the values are bf16 already), then accumulate.
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint4 src = vr[j >> 1];
+        const i16x4 va = (j & 1) ? as_i16x4(src.z, src.w) : as_i16x4(src.x, src.y);
+        const f32x4 d = mfma_16x16x16_bf16(va, ident, f32x4{0.f, 0.f, 0.f, 0.f});
+        const i16x4 vt = as_i16x4(pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3]));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t][j] = mfma_16x16x16_bf16(vt, pf[t], acc[t][j] * alpha[t]);
+      }
+      after_pv();
+  };
+
+#if ASPIRE_PIPE == 0
+  // One K/V register buffer pipelined at half-page granularity: the next
   // page's K is requested as soon as this page's QK^T has consumed K, and its V
-  // as soon as P.V has consumed V, so about one page stays in flight per wave
-  // with 32 VGPRs of staging.
-  uint4 kr[4], vr[4];
+  // as soon as P.V has consumed each V slice (about one page in flight per
+  // wave, 32 VGPRs). Prologue and loop share one block so the loop head sees a
+  // single, straight-line load order.
+  if (pb < pe) {
+    uint4 kr[4], vr[4];
+    {
+      const int64_t phys = page_id(pb);
+      const bool ok = pb * 16 + r < kv_len;
+      load_k(phys, ok, kr);
+      __builtin_amdgcn_sched_barrier(0);
+      load_v(phys, ok, vr);
+    }
+    int64_t id_ahead = page_id(pb + 1);
+    int pg = pb;
+    do {
+      const bool has_next = pg + 1 < pe;
+      const int64_t next_phys = id_ahead;
+      id_ahead = page_id(pg + 2);
+      // Issued unconditionally (straight-line code keeps the wait counts
+      // exact); past the item's last page the out-of-range offset returns zeros.
+      const bool next_ok = has_next && (pg + 1) * 16 + r < kv_len;
+      page_body(pg, kr, vr, [&] { load_k(next_phys, next_ok, kr); }, [&] { load_v(next_phys, next_ok, vr); });
+    } while (++pg < pe);
+  }
+#else
+  auto nothing = [] {};
+  // Two K/V register buffers: the next page's K and V are requested before the
+  // current page is computed (up to two pages in flight, 64 VGPRs).
+  uint4 ka[4], va[4], kb[4], vb[4];
   if (pb < pe) {
     const int64_t phys = page_id(pb);
     const bool ok = pb * 16 + r < kv_len;
-    load_k(p, phys, g, r, grp, ok, kr);
-    load_v(p, phys, g, r, grp, ok, vr);
+    load_k(phys, ok, ka);
+    load_v(phys, ok, va);
   }
-  for (int pg = pb; pg < pe; ++pg) {
-    const bool has_next = pg + 1 < pe;
-    const int64_t next_phys = has_next ? page_id(pg + 1) : 0;
-    const bool next_ok = (pg + 1) * 16 + r < kv_len;
-    const int base_pos = pg * 16 + grp * 4;
-
-    f32x4 s[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) s[t] = mfma_16x16x32_bf16(as_bf16x8(kr[c]), qf[t][c], s[t]);
+  for (int pg = pb; pg < pe; pg += 2) {
+    if (pg + 1 < pe) {
+      const int64_t phys = page_id(pg + 1);
+      const bool ok = (pg + 1) * 16 + r < kv_len;
+      load_k(phys, ok, kb);
+      load_v(phys, ok, vb);
     }
-    if (has_next) load_k(p, next_phys, g, r, grp, next_ok, kr);
-
-    i16x4 pf[NT];
-    float alpha[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      if (do_dump && row_qi[t] >= 0) {
-        const int qi = row_qi[t];
-        int slot = -1;
-        if (p.dump_kind == 2)
-          slot = qi == 0 ? 0 : (qi == it.q_len - 1 ? 1 : -1);
-        else if (qi == it.q_len - 1)
-          slot = 0;
-        if (slot >= 0) {
-          const int head = g * G + (t * 16 + r - qi * G);
-          const int64_t base =
-              (int64_t(b * p.dump_heads + head) * dump_slots + slot) * p.dump_stride;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (base_pos + i < kv_len) store_dump(p, base + base_pos + i, s[t][i]);
-        }
-      }
-      if (do_score && t == 0) {
-        float rs = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) rs += (base_pos + i < kv_len) ? s[t][i] : 0.f;
-        rs += shfl_xor_f(rs, 16);
-        rs += shfl_xor_f(rs, 32);
-        const int cnt = min(16, kv_len - pg * 16);
-        float val = (r < G) ? rs / float(cnt) : kNegInf;
-        val = fmaxf(val, shfl_xor_f(val, 1));
-        val = fmaxf(val, shfl_xor_f(val, 2));
-        val = fmaxf(val, shfl_xor_f(val, 4));
-        val = fmaxf(val, shfl_xor_f(val, 8));
-        if (lane == 0) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + pg] = val;
-      }
-
-      float x[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        x[i] = (base_pos + i <= limit[t]) ? s[t][i] * p.scale_log2 : kNegInf;
-      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
-      const float m_new = fmaxf(m[t], mx);
-      float a = 1.f;
-      float pv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (m_new != kNegInf) {
-        a = __builtin_amdgcn_exp2f(m[t] - m_new);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
-      }
-      l[t] = l[t] * a + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
-      m[t] = m_new;
-      alpha[t] = a;
-      pf[t] = as_i16x4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]));
+    page_body(pg, ka, va, nothing, nothing);
+    if (pg + 1 >= pe) break;
+    if (pg + 2 < pe) {
+      const int64_t phys = page_id(pg + 2);
+      const bool ok = (pg + 2) * 16 + r < kv_len;
+      load_k(phys, ok, ka);
+      load_v(phys, ok, va);
     }
-
-    // O^T += V^T P^T, one 16-dim slice at a time: transpose the slice with an
-    // exact identity MFMA (the values are bf16 already), then accumulate.
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint4 src = vr[j >> 1];
-      const i16x4 va = (j & 1) ? as_i16x4(src.z, src.w) : as_i16x4(src.x, src.y);
-      const f32x4 d = mfma_16x16x16_bf16(va, ident, f32x4{0.f, 0.f, 0.f, 0.f});
-      const i16x4 vt = as_i16x4(pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3]));
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t][j] = mfma_16x16x16_bf16(vt, pf[t], acc[t][j] * alpha[t]);
-    }
-    if (has_next) load_v(p, next_phys, g, r, grp, next_ok, vr);
+    page_body(pg + 1, kb, vb, nothing, nothing);
   }
+#endif
 
   // Epilogue: normalise and write the final output or the fp32 partial.
 #pragma unroll
@@ -278,7 +364,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       const int qi = row / G;
       const int head = g * G + (row - qi * G);
       const int token = it.q_start + qi;
-      uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + grp * 32;
+      uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const f32x4 a0 = acc[t][2 * c];
@@ -288,16 +374,17 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
         w.y = pack_bf16x2_rne(a0[2] * inv, a0[3] * inv);
         w.z = pack_bf16x2_rne(a1[0] * inv, a1[1] * inv);
         w.w = pack_bf16x2_rne(a1[2] * inv, a1[3] * inv);
-        reinterpret_cast<uint4*>(dst)[c] = w;
+        *reinterpret_cast<uint4*>(dst + dim_off(grp, c)) = w;
       }
       if (grp == 0 && p.lse != nullptr) p.lse[int64_t(token) * p.hq + head] = lse_v;
     } else {
       const int64_t prow = int64_t(it.partial_row) + row;
-      float* dst = p.part_o + prow * kHeadDim + grp * 32;
+      float* dst = p.part_o + prow * kHeadDim;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const f32x4 a = acc[t][j];
-        reinterpret_cast<float4*>(dst)[j] = make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+        *reinterpret_cast<float4*>(dst + dim_off(grp, j >> 1) + 4 * (j & 1)) =
+            make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
       }
       if (grp == 0) p.part_lse[prow] = lse_v;
     }
@@ -342,44 +429,83 @@ void attention_kernel(AttnParams p) {
   }
 }
 
-// Merge of split segments: thread e of a merge item handles 4 dims of one row.
+// Merge of split segments: one wave per (merge item, query row). Lane i reads
+// the LSE of piece i; the max and the weights are reduced across the wave, then
+// lane l accumulates dims 2l, 2l+1 over the pieces (loads issued back to back).
+constexpr int kMergeRows = 16 * kMaxRowTiles;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
 __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
-  const int num_merge = p.plan[3];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int waves = gridDim.x * 4;
+  const int num_merge = wave_uniform(p.plan[3]);
   const MergeItem* items = reinterpret_cast<const MergeItem*>(p.plan + p.merge_off);
-  for (int mi = blockIdx.x; mi < num_merge; mi += gridDim.x) {
-    const MergeItem it = items[mi];
-    const int g = it.bg & 255;
-    for (int e = threadIdx.x; e < it.rows * 32; e += blockDim.x) {
-      const int row = e >> 5;
-      const int d4 = (e & 31) * 4;
-      float mx = kNegInf;
-      for (int k = 0; k < it.num_pieces; ++k)
-        mx = fmaxf(mx, p.part_lse[int64_t(it.first_partial_row) + int64_t(k) * it.rows + row]);
-      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f, sum = 0.f;
-      if (mx != kNegInf) {
-        for (int k = 0; k < it.num_pieces; ++k) {
-          const int64_t pr = int64_t(it.first_partial_row) + int64_t(k) * it.rows + row;
-          const float w = __builtin_amdgcn_exp2f(p.part_lse[pr] - mx);
-          const float4 v = *reinterpret_cast<const float4*>(p.part_o + pr * kHeadDim + d4);
-          sum += w;
+  for (int u = wave; u < num_merge * kMergeRows; u += waves) {
+    const int mi = u / kMergeRows;
+    const int row = u - mi * kMergeRows;
+    const int rows = wave_uniform(items[mi].rows);
+    if (row >= rows) continue;
+    const int pieces = wave_uniform(items[mi].num_pieces);
+    const int64_t first = wave_uniform(items[mi].first_partial_row) + int64_t(row);
+    float mx = kNegInf;
+    for (int k0 = 0; k0 < pieces; k0 += 64) {
+      const int k = k0 + lane;
+      mx = fmaxf(mx, k < pieces ? p.part_lse[first + int64_t(k) * rows] : kNegInf);
+    }
+    mx = wave_max(mx);
+    float o0 = 0.f, o1 = 0.f, sum = 0.f;
+    if (mx != kNegInf) {
+      for (int k0 = 0; k0 < pieces; k0 += 64) {
+        const int k = k0 + lane;
+        const float wk = k < pieces ? __builtin_amdgcn_exp2f(p.part_lse[first + int64_t(k) * rows] - mx) : 0.f;
+        sum += wave_sum(wk);
+        const int n = min(64, pieces - k0);
+        int j = 0;
+        for (; j + 4 <= n; j += 4) {
+          float2 v[4];
+          float w[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            v[x] = *reinterpret_cast<const float2*>(p.part_o + (first + int64_t(k0 + j + x) * rows) * kHeadDim +
+                                                    2 * lane);
+            w[x] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), j + x));
+          }
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            o0 += w[x] * v[x].x;
+            o1 += w[x] * v[x].y;
+          }
+        }
+        for (; j < n; ++j) {
+          const float2 v =
+              *reinterpret_cast<const float2*>(p.part_o + (first + int64_t(k0 + j) * rows) * kHeadDim + 2 * lane);
+          const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), j));
           o0 += w * v.x;
           o1 += w * v.y;
-          o2 += w * v.z;
-          o3 += w * v.w;
         }
       }
-      const float inv = sum > 0.f ? 1.f / sum : 0.f;
-      const int qi = row / p.group;
-      const int head = g * p.group + (row - qi * p.group);
-      const int token = it.q_start + qi;
-      uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + d4;
-      uint2 w2;
-      w2.x = pack_bf16x2_rne(o0 * inv, o1 * inv);
-      w2.y = pack_bf16x2_rne(o2 * inv, o3 * inv);
-      *reinterpret_cast<uint2*>(dst) = w2;
-      if (d4 == 0 && p.lse != nullptr)
-        p.lse[int64_t(token) * p.hq + head] = sum > 0.f ? mx + __builtin_log2f(sum) : kNegInf;
     }
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    const int G = p.group;
+    const int qi = row / G;
+    const int g = wave_uniform(items[mi].bg) & 255;
+    const int head = g * G + (row - qi * G);
+    const int token = wave_uniform(items[mi].q_start) + qi;
+    uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + 2 * lane;
+    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2_rne(o0 * inv, o1 * inv);
+    if (lane == 0 && p.lse != nullptr)
+      p.lse[int64_t(token) * p.hq + head] = sum > 0.f ? mx + __builtin_log2f(sum) : kNegInf;
   }
 }
 
@@ -443,6 +569,8 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
                        a->cache_stride_h % 8 == 0,
                    "strides must be multiples of 8 elements");
   ASPIRE_CHECK_ARG(a->dump_kind >= 0 && a->dump_kind <= 2, "dump_kind must be 0, 1 or 2");
+  ASPIRE_CHECK_ARG(a->cache_stride_t > 0 && (15 * a->cache_stride_t + kHeadDim) * 2 < (int64_t(1) << 30),
+                   "cache token stride too large for 32-bit buffer offsets");
   ASPIRE_CHECK_ARG(a->dump_kind == 0 || (a->dump != nullptr && a->dump_kv_stride > 0 &&
                                          a->dump_num_heads > 0),
                    "dump buffer, stride and head count required");
@@ -504,8 +632,7 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
     mp.lse = p.lse;
     mp.hq = p.hq;
     mp.group = p.group;
-    const int blocks = std::min(layout->max_merge, 2048);
-    hipLaunchKernelGGL(merge_kernel, dim3(blocks), dim3(256), 0, s, mp);
+    hipLaunchKernelGGL(merge_kernel, dim3(1024), dim3(256), 0, s, mp);
     ASPIRE_CHECK_LAUNCH();
   }
   return ASPIRE_OK;

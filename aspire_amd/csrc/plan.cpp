@@ -7,12 +7,15 @@
 // captured in a HIP graph replays correctly after any later plan.
 //
 // Decomposition (stream-K): the segments of a class are laid end to end as a
-// sequence of page-heads (one page of one kv head = 16 tokens x 2 x 256 B);
-// wave w takes the contiguous range [w*T/W, (w+1)*T/W). A segment cut by a
-// range boundary is split into pieces that write fp32 partial (o, lse) rows;
-// a merge item per split segment combines them. This balances HBM traffic
-// per wave exactly and creates at most two split pieces per wave, unlike a
-// fixed chunk length.
+// sequence of pages; slot j takes the contiguous range [j*T/S, (j+1)*T/S). A
+// segment cut by a range boundary is split into pieces that write fp32
+// partial (o, lse) rows; a merge item per split (row, kv head) combines them.
+// This balances HBM traffic per wave exactly and creates at most two split
+// pieces per slot, unlike a fixed chunk length. With row-shared page lists a
+// slot is a group of num_kv_heads consecutive waves and a segment is a whole
+// row (wave g of the group streams kv head g of the same pages at the same
+// time); with per-(row, kv head) lists a slot is one wave and a segment one
+// (row, kv head).
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -113,6 +116,14 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
   sc.items.clear();
   sc.merges.clear();
 
+  // Row-shared page lists are planned head-aligned: the stream-K unit is a
+  // whole page (all kv heads) and a slot is a group of num_kv_heads
+  // consecutive waves, wave g of the group streaming kv head g. Every head of
+  // a page is then read at about the same time by waves dispatched together,
+  // which keeps the page's 64 KB of DRAM traffic together. Per-head lists are
+  // planned per (row, kv head) segment with single-wave slots.
+  const bool aligned = !per_head_lists && W % num_kv_heads == 0;
+  const int hpu = aligned ? num_kv_heads : 1;
   int max_rows = 0;
   int num_segments = 0;
   for (int b = 0; b < batch; ++b) {
@@ -126,7 +137,7 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
     }
     max_rows = std::max(max_rows, rows);
     const int cls = (rows - 1) / 16;
-    for (int g = 0; g < num_kv_heads; ++g) {
+    for (int g = 0; g < num_kv_heads; g += hpu) {
       const int s = per_head_lists ? b * num_kv_heads + g : b;
       const int kvl = kv_len[s];
       const int list_pages = kv_indptr[s + 1] - kv_indptr[s];
@@ -142,10 +153,7 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
       }
       sc.segs[cls].push_back(
           Segment{qo_indptr[b], q_len, kvl, kv_indptr[s], np, (b << 8) | g, rows});
-      ++num_segments;
-      if (!per_head_lists && g == 0) {
-        // the row-shared list is the same for every kv head; nothing more to check
-      }
+      num_segments += hpu;
     }
   }
 
@@ -158,9 +166,10 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
     const auto& segs = sc.segs[c];
     int64_t T = 0;
     for (const auto& s : segs) T += s.npages;
-    total_pages += T;
-    // Waves actually used: enough that each streams >= kMinPagesPerWave pages.
-    int64_t w_eff = std::max<int64_t>(1, std::min<int64_t>(W, T / kMinPagesPerWave));
+    total_pages += T * hpu;
+    const int64_t slots = W / hpu;
+    // Slots actually used: enough that each streams >= kMinPagesPerWave pages.
+    int64_t s_eff = std::max<int64_t>(1, std::min<int64_t>(slots, T / kMinPagesPerWave));
     // Shrink until the split pieces' partial rows fit the float workspace.
     for (;;) {
       sc.items.clear();
@@ -170,41 +179,51 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
       int zero_rr = 0;
       for (const auto& s : segs) {
         if (s.npages == 0) {
-          WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, 0, 0, s.bg, -1};
-          sc.items.emplace_back(static_cast<int32_t>(zero_rr++ % w_eff), it);
+          const int64_t slot = zero_rr++ % s_eff;
+          for (int gg = 0; gg < hpu; ++gg) {
+            WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, 0, 0, s.bg + gg, -1};
+            sc.items.emplace_back(static_cast<int32_t>(slot * hpu + gg), it);
+          }
           continue;
         }
         const int64_t a = seg_off, e = seg_off + s.npages;
-        // wave containing global page a: largest w with floor(w*T/w_eff) <= a
-        int64_t w_lo = (a * w_eff) / T;
-        while (w_lo > 0 && (w_lo * T) / w_eff > a) --w_lo;
-        while (w_lo + 1 < w_eff && ((w_lo + 1) * T) / w_eff <= a) ++w_lo;
-        int64_t w_hi = ((e - 1) * w_eff) / T;
-        while (w_hi > 0 && (w_hi * T) / w_eff > e - 1) --w_hi;
-        while (w_hi + 1 < w_eff && ((w_hi + 1) * T) / w_eff <= e - 1) ++w_hi;
-        const int pieces = static_cast<int>(w_hi - w_lo + 1);
-        const int first_row = pieces > 1 ? static_cast<int>(pr) : -1;
-        for (int64_t w = w_lo; w <= w_hi; ++w) {
-          const int64_t wb = std::max(a, (w * T) / w_eff);
-          const int64_t we = std::min(e, ((w + 1) * T) / w_eff);
-          WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, static_cast<int32_t>(wb - a),
-                      static_cast<int32_t>(we - a), s.bg,
-                      pieces > 1 ? static_cast<int32_t>(pr) : -1};
-          if (pieces > 1) pr += s.rows;
-          sc.items.emplace_back(static_cast<int32_t>(w), it);
+        // slot containing global page a: largest j with floor(j*T/s_eff) <= a
+        int64_t j_lo = (a * s_eff) / T;
+        while (j_lo > 0 && (j_lo * T) / s_eff > a) --j_lo;
+        while (j_lo + 1 < s_eff && ((j_lo + 1) * T) / s_eff <= a) ++j_lo;
+        int64_t j_hi = ((e - 1) * s_eff) / T;
+        while (j_hi > 0 && (j_hi * T) / s_eff > e - 1) --j_hi;
+        while (j_hi + 1 < s_eff && ((j_hi + 1) * T) / s_eff <= e - 1) ++j_hi;
+        const int pieces = static_cast<int>(j_hi - j_lo + 1);
+        // partial rows: head gg's pieces are contiguous, first[gg] + k * rows
+        const int64_t first = pr;
+        if (pieces > 1) pr += int64_t(hpu) * pieces * s.rows;
+        for (int64_t j = j_lo; j <= j_hi; ++j) {
+          const int64_t wb = std::max(a, (j * T) / s_eff);
+          const int64_t we = std::min(e, ((j + 1) * T) / s_eff);
+          const int64_t k = j - j_lo;
+          for (int gg = 0; gg < hpu; ++gg) {
+            const int64_t prow = pieces > 1 ? first + (int64_t(gg) * pieces + k) * s.rows : -1;
+            WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, static_cast<int32_t>(wb - a),
+                        static_cast<int32_t>(we - a), s.bg + gg, static_cast<int32_t>(prow)};
+            sc.items.emplace_back(static_cast<int32_t>(j * hpu + gg), it);
+          }
         }
         if (pieces > 1)
-          sc.merges.push_back(MergeItem{s.q_start, s.q_len, s.bg, first_row, pieces, s.rows, 0, 0});
+          for (int gg = 0; gg < hpu; ++gg)
+            sc.merges.push_back(MergeItem{s.q_start, s.q_len, s.bg + gg,
+                                          static_cast<int32_t>(first + int64_t(gg) * pieces * s.rows),
+                                          pieces, s.rows, 0, 0});
         seg_off = e;
       }
-      if (pr <= L.partial_rows_cap || w_eff == 1) {
+      if (pr <= L.partial_rows_cap || s_eff == 1) {
         if (pr > L.partial_rows_cap)
           return fail(ASPIRE_ERR_CAPACITY, "aspire_plan_build: float workspace too small");
         partial_rows = pr;
         break;
       }
       sc.merges.resize(merges_before);
-      w_eff = std::max<int64_t>(1, w_eff / 2);
+      s_eff = std::max<int64_t>(1, s_eff / 2);
     }
     if (static_cast<int64_t>(sc.items.size()) > L.max_items) {
       set_error("aspire_plan_build: class %d needs %zu work items, capacity %d", c,

@@ -1,0 +1,297 @@
+"""Benchmark of one mixed draft/verify attention layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1] [--no-cpu-baseline]
+
+A step is one pass of the hot path over one batch resident in HBM: the paged
+KV append of the batch's new tokens followed by mixed draft/verify attention
+(including the split-KV merge). Default workload: BASELINE config 1, the
+Qwen3-8B-shape layer (32 q / 8 kv heads, head_dim 128, bf16, 16-token pages),
+batch 32 x 32768-token contexts, 16 drafting rows (q_len 1 over 128 selected
+pages) and 16 verifying rows (q_len 4, causal, full cache). ``--config 2`` runs
+the Qwen3-8B refresh layer (batch 64, contexts U[8192, 32768], full attention
+for every single-query row with the per-KV-head key-mean page scores and the
+top-128 page selection).
+
+value = algorithmic HBM bytes of the step / step time (GB/s). The roofline
+object reports the dominant kernel (mixed attention) alone: its algorithmic
+bytes per launch (KV pages read + q + o + page ids) over its average launch
+time, measured with HIP events on the stream it runs on. The CPU baseline
+times the repository's CPU oracle (torch fp32) on a bounded sample of rows of
+the same workload on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0  # MI355X published HBM3E bandwidth
+TRAFFIC_NOTE = None
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=1, choices=[1, 2])
+    ap.add_argument("--waves-per-cu", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def timed(fn, steps, stream):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms
+
+
+def attention_only(w, q, cache, out):
+    """Launch only the attention kernels of w's current plan (no merge), as run() would."""
+    import ctypes
+
+    from aspire_amd import _lib
+
+    k_cache, v_cache = cache[:, 0], cache[:, 1]
+    a = _lib.AttentionArgs()
+    a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.kv_cache = k_cache.data_ptr()
+    a.cache_stride_p = k_cache.stride(0)
+    a.cache_stride_kv = (v_cache.data_ptr() - k_cache.data_ptr()) // 2
+    a.cache_stride_t, a.cache_stride_h = k_cache.stride(1), k_cache.stride(2)
+    a.kv_indices = w._kv_indices.data_ptr()
+    a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.plan_dev = w._int_workspace.data_ptr()
+    a.float_ws = w._float_workspace.data_ptr()
+    a.num_qo_heads, a.num_kv_heads, a.head_dim, a.page_size = w._num_qo_heads, w._num_kv_heads, 128, 16
+    a.sm_scale, a.causal = 1.0 / 128 ** 0.5, 1
+    info = w.plan_info
+    a.class_mask = sum(1 << c for c in range(3) if info.num_items[c] > 0)
+    a.launch_merge = 0
+    layout = w._layout
+
+    def launch():
+        rc = _lib.lib().aspire_attention_run(ctypes.byref(layout), ctypes.byref(a), _lib.stream_of(q))
+        _lib.check(rc, "attention_only")
+
+    return launch
+
+
+def cpu_baseline(step_cpu_fn, budget_s):
+    """Time the CPU oracle on rows until ``budget_s`` of work; returns (GB/s, bytes, seconds, rows)."""
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    done_bytes, t_total, rows = 0, 0.0, []
+    for row, fn, nbytes in step_cpu_fn():
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        done_bytes += nbytes
+        t_total += dt
+        rows.append(row)
+        if t_total >= budget_s:
+            break
+    return done_bytes / t_total / 1e9, done_bytes, t_total, rows, threads
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import aspire_amd.attention.kv_ops  # noqa: F401
+    from aspire_amd import _lib
+    from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
+    from aspire_amd.backends.page_selector import KeyMeanPageSelector
+    from aspire_amd.workloads import PAGE, config1, config2
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(_lib.build_info())
+    t0 = time.time()
+    step = config1(device=dev) if args.config == 1 else config2(device=dev)
+    torch.cuda.synchronize()
+    log(f"workload built in {time.time() - t0:.1f}s: batch {step.batch}, tokens {step.total_tokens}, "
+        f"pool {step.cache.shape[0]} pages ({step.cache.numel() * 2 / 2**30:.2f} GiB)")
+    cache = step.cache
+    w = HolisticAttentionWrapper(torch.empty(1, device=dev), "NHD", waves_per_cu=args.waves_per_cu)
+    w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, step.hq, step.hkv, 128, PAGE,
+           causal=True)
+    # host planning cost (plan_host: C++ planner + async upload), measured on its own
+    reps = 20
+    tp = time.perf_counter()
+    for _ in range(reps):
+        w.plan_host(step.qo_indptr_host, step.kv_indptr_host, step.kv_len_host, step.kv_indices, step.hq,
+                    step.hkv, 128, PAGE, causal=True)
+    plan_us = (time.perf_counter() - tp) / reps * 1e6
+    torch.cuda.synchronize()
+    info = w.plan_info
+    log(f"plan: items {list(info.num_items)}, merges {info.num_merge}, partial rows {info.partial_rows}, "
+        f"host {plan_us:.1f} us/plan")
+
+    out = torch.empty_like(step.q)
+    stream = torch.cuda.current_stream(dev)
+    nbytes = step.algorithmic_bytes(include_append=args.config == 1)
+    selector = None
+    if args.config == 2:
+        max_pages = int(step.block_table.shape[1])
+        selector = KeyMeanPageSelector(step.batch, step.hkv, max_pages, k=128, L=0, device=dev)
+        npg = torch.from_numpy((step.ctx_len + PAGE - 1) // PAGE).to(torch.int32).to(dev)
+        nbytes["selection"] = step.batch * step.hkv * 128 * 4
+        nbytes["total"] += nbytes["selection"]
+
+        def run_step():
+            w.run(step.q, cache, out=out, page_scores=selector.page_scores)
+            selector.select(npg, step.block_table)
+    else:
+        def run_step():
+            torch.ops.mylib.update_kv_padded(step.k_new, step.v_new, step.qo_indptr, cache, step.kv_indices,
+                                             step.kv_indptr, step.last_page_len, PAGE)
+            w.run(step.q, cache, out=out)
+
+    for _ in range(args.warmup):
+        run_step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    ms = timed(run_step, args.steps, stream)
+    value = nbytes["total"] / (ms * 1e-3) / 1e9
+
+    # dominant kernel alone: mixed attention (no merge), same plan, same stream
+    attn = attention_only(w, step.q, cache, out)
+    for _ in range(3):
+        attn()
+    attn_ms = timed(attn, args.steps, stream)
+    attn_bytes = nbytes["kv"] + nbytes["qo"] + nbytes["indices"]
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    log(f"step {ms * 1e3:.1f} us -> {value:.0f} GB/s; attention kernel {attn_ms * 1e3:.1f} us -> "
+        f"{achieved:.0f} GB/s ({achieved / PEAK_HBM_GBS:.1%} of 8 TB/s)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = run_cpu_baseline(step, args.cpu_seconds)
+
+    tokens = step.total_tokens
+    if args.config == 1:
+        workload = ("config1: Qwen3-8B-shape mixed layer (32 q / 8 kv heads, head_dim 128, bf16, 16-token pages), "
+                    "batch 32 x 32768-token contexts, 16 draft rows (q_len 1 over 128 selected pages) + 16 verify "
+                    "rows (q_len 4, causal, full cache); KV append of the 80 new tokens + attention")
+        metric = "mixed-attn layer HBM GB/s (Qwen3-8B shape, B=32 x 32k, 16 draft + 16 verify)"
+    else:
+        workload = ("config2: Qwen3-8B-shape refresh layer, batch 64, contexts U[8192, 32768], full attention for "
+                    "64 single-query rows + per-KV-head key-mean page scores + top-128 selection")
+        metric = "refresh-layer HBM GB/s (Qwen3-8B shape, B=64, ctx U[8k,32k])"
+    line = {
+        "metric": metric,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/Q with per-page key bias; random-permutation page pool)",
+        "config": {
+            "workload": workload,
+            "batch": step.batch,
+            "context_tokens": int(step.ctx_len.max()),
+            "tokens_per_step": tokens,
+            "algorithmic_bytes": nbytes,
+            "hbm_fraction_of_peak": round(value / PEAK_HBM_GBS, 4),
+            "decode_tokens_per_s_layer": round(tokens / (ms * 1e-3), 1),
+            "plan_host_us": round(plan_us, 1),
+            "plan": {"items": list(info.num_items), "merges": info.num_merge, "waves": w._layout.num_waves},
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attention_kernel (mixed draft/verify, row-tile class 1)",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": TRAFFIC_NOTE,
+            "kernel_us": round(attn_ms * 1e3, 2),
+            "bytes_per_launch": attn_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def run_cpu_baseline(step, budget_s):
+    """CPU oracle (append + attention, torch fp32) on rows of the same workload."""
+    from oracle.append import paged_kv_append
+    from oracle.attention import paged_attention
+
+    qo = step.qo_indptr_host.numpy()
+    kvp = step.kv_indptr_host.numpy()
+    kvl = step.kv_len_host.numpy()
+    idx = step.kv_indices.cpu()
+    order = []
+    # alternate verify and draft rows (verify rows dominate the bytes)
+    ver = [b for b in range(step.batch) if not step.is_draft[b]]
+    dra = [b for b in range(step.batch) if step.is_draft[b]]
+    for i in range(max(len(ver), len(dra))):
+        order += ([ver[i]] if i < len(ver) else []) + ([dra[i]] if i < len(dra) else [])
+
+    def rows():
+        for b in order:
+            pages = idx[kvp[b] : kvp[b + 1]].long()
+            small = step.cache[pages.to(step.cache.device)].cpu()
+            q = step.q[qo[b] : qo[b + 1]].cpu()
+            kn = step.k_new[qo[b] : qo[b + 1]].cpu()
+            vn = step.v_new[qo[b] : qo[b + 1]].cpu()
+            n_pages = int(kvp[b + 1] - kvp[b])
+            t = int(qo[b + 1] - qo[b])
+            local_idx = np.arange(n_pages, dtype=np.int32)
+            lpl = np.array([(int(kvl[b]) - 1) % 16 + 1], dtype=np.int32)
+            nbytes = int(kvl[b]) * step.hkv * 128 * 4 + t * step.hq * 128 * 4 + t * step.hkv * 128 * 8 + n_pages * 4
+
+            def fn(small=small, q=q, kn=kn, vn=vn, n_pages=n_pages, t=t, local_idx=local_idx, lpl=lpl, b=b):
+                cache_bits = small.view(torch.int16).numpy()
+                newc = paged_kv_append(kn.view(torch.int16).numpy(), vn.view(torch.int16).numpy(),
+                                       np.array([0, t]), cache_bits, local_idx, np.array([0, n_pages]), lpl, 16)
+                c = torch.from_numpy(newc).view(torch.bfloat16)
+                paged_attention(q, c, [0, t], [0, n_pages], torch.from_numpy(local_idx), [int(kvl[b])],
+                                num_kv_heads=step.hkv)
+
+            yield b, fn, nbytes
+
+    gbs, done, secs, used, threads = cpu_baseline(rows, budget_s)
+    log(f"cpu baseline: {gbs:.2f} GB/s over {len(used)} rows in {secs:.1f}s on {threads} threads")
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(used)} rows of the same workload (rows {used}), KV append + attention through the CPU "
+                  f"oracle (torch fp32), {done / 1e9:.2f} GB of algorithmic bytes in {secs:.1f} s",
+    }
+
+
+if __name__ == "__main__":
+    main()
