@@ -36,7 +36,22 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X published HBM3E bandwidth
-TRAFFIC_NOTE = None
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def measured_traffic(config: int):
+    """HBM bytes per attention launch from the committed rocprofv3 counter summary, if present.
+
+    profiles/attention_config<N>_traffic.txt holds the calibrated FETCH_SIZE +
+    WRITE_SIZE of the attention kernel (see the file for the commands).
+    """
+    path = os.path.join(PROFILES, f"attention_config{config}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def log(*a):
@@ -52,6 +67,8 @@ def parse():
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (read + write) for rocprofv3 counter calibration")
     return ap.parse_args()
 
 
@@ -188,6 +205,15 @@ def main():
     log(f"step {ms * 1e3:.1f} us -> {value:.0f} GB/s; attention kernel {attn_ms * 1e3:.1f} us -> "
         f"{achieved:.0f} GB/s ({achieved / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
+    if args.calibrate_copy:
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev).random_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = run_cpu_baseline(step, args.cpu_seconds)
@@ -233,7 +259,7 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": TRAFFIC_NOTE,
+            "traffic": measured_traffic(args.config),
             "kernel_us": round(attn_ms * 1e3, 2),
             "bytes_per_launch": attn_bytes,
         },
