@@ -399,10 +399,10 @@ struct Occupancy {
 };
 
 template <int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Occupancy<NT>::waves)))
+__global__ __launch_bounds__(64 * kAttnWavesPerBlock) __attribute__((amdgpu_waves_per_eu(Occupancy<NT>::waves)))
 void attention_kernel(AttnParams p) {
   const int lane = threadIdx.x & 63;
-  const int wave = wave_uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int wave = wave_uniform(blockIdx.x * kAttnWavesPerBlock + (threadIdx.x >> 6));
   if (wave >= p.num_waves) return;
   const int32_t* indptr = p.plan + p.indptr_off;
   const int w0 = wave_uniform(indptr[wave]);
@@ -429,23 +429,12 @@ void attention_kernel(AttnParams p) {
   }
 }
 
-// Merge of split segments: one wave per (merge item, query row). Lane i reads
-// the LSE of piece i; the max and the weights are reduced across the wave, then
-// lane l accumulates dims 2l, 2l+1 over the pieces (loads issued back to back).
+// Merge of split segments: one wave per (merge item, query row); lane l owns
+// dims 2l, 2l+1 and every lane reads the (wave-uniform) piece LSEs.
 constexpr int kMergeRows = 16 * kMaxRowTiles;
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-
 __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
+  constexpr int kChunk = 16;  // pieces whose loads are issued together
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int waves = gridDim.x * 4;
@@ -458,43 +447,35 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
     if (row >= rows) continue;
     const int pieces = wave_uniform(items[mi].num_pieces);
     const int64_t first = wave_uniform(items[mi].first_partial_row) + int64_t(row);
-    float mx = kNegInf;
-    for (int k0 = 0; k0 < pieces; k0 += 64) {
-      const int k = k0 + lane;
-      mx = fmaxf(mx, k < pieces ? p.part_lse[first + int64_t(k) * rows] : kNegInf);
-    }
-    mx = wave_max(mx);
-    float o0 = 0.f, o1 = 0.f, sum = 0.f;
-    if (mx != kNegInf) {
-      for (int k0 = 0; k0 < pieces; k0 += 64) {
-        const int k = k0 + lane;
-        const float wk = k < pieces ? __builtin_amdgcn_exp2f(p.part_lse[first + int64_t(k) * rows] - mx) : 0.f;
-        sum += wave_sum(wk);
-        const int n = min(64, pieces - k0);
-        int j = 0;
-        for (; j + 4 <= n; j += 4) {
-          float2 v[4];
-          float w[4];
+    // Running (max, sum, o) over chunks of pieces; within a chunk every LSE and
+    // partial load is issued before any is used (one memory round trip).
+    float mx = kNegInf, sum = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int k0 = 0; k0 < pieces; k0 += kChunk) {
+      const int n = min(kChunk, pieces - k0);
+      float lse[kChunk];
+      float2 v[kChunk];
 #pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            v[x] = *reinterpret_cast<const float2*>(p.part_o + (first + int64_t(k0 + j + x) * rows) * kHeadDim +
-                                                    2 * lane);
-            w[x] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), j + x));
-          }
-#pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            o0 += w[x] * v[x].x;
-            o1 += w[x] * v[x].y;
-          }
-        }
-        for (; j < n; ++j) {
-          const float2 v =
-              *reinterpret_cast<const float2*>(p.part_o + (first + int64_t(k0 + j) * rows) * kHeadDim + 2 * lane);
-          const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), j));
-          o0 += w * v.x;
-          o1 += w * v.y;
-        }
+      for (int x = 0; x < kChunk; ++x) {
+        const int64_t pr = first + int64_t(k0 + min(x, n - 1)) * rows;
+        lse[x] = x < n ? p.part_lse[pr] : kNegInf;
+        v[x] = *reinterpret_cast<const float2*>(p.part_o + pr * kHeadDim + 2 * lane);
       }
+      float cmx = mx;
+#pragma unroll
+      for (int x = 0; x < kChunk; ++x) cmx = fmaxf(cmx, lse[x]);
+      if (cmx == kNegInf) continue;
+      const float scale = __builtin_amdgcn_exp2f(mx - cmx);  // 0 when mx = -inf
+      sum *= scale;
+      o0 *= scale;
+      o1 *= scale;
+#pragma unroll
+      for (int x = 0; x < kChunk; ++x) {
+        const float w = __builtin_amdgcn_exp2f(lse[x] - cmx);  // 0 for padding / empty pieces
+        sum += w;
+        o0 += w * v[x].x;
+        o1 += w * v[x].y;
+      }
+      mx = cmx;
     }
     const float inv = sum > 0.f ? 1.f / sum : 0.f;
     const int G = p.group;
@@ -607,17 +588,17 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
   p.page_scores = a->page_scores;
   p.ps_stride = a->page_score_stride;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((layout->num_waves + 3) / 4);
+  const dim3 grid((layout->num_waves + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock);
   for (int c = 0; c < 3; ++c) {
     if (!(a->class_mask & (1 << c))) continue;
     p.indptr_off = off.indptr[c];
     p.items_off = off.items[c];
     if (c == 0)
-      hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
     else if (c == 1)
-      hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
     else
-      hipLaunchKernelGGL(attention_kernel<3>, grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL(attention_kernel<3>, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
     ASPIRE_CHECK_LAUNCH();
   }
   if (a->launch_merge) {

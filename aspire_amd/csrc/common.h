@@ -51,6 +51,14 @@ inline int fail(int code, const char* msg) {
 constexpr int kHeadDim = 128;
 constexpr int kPage = 16;
 constexpr int kMaxRowTiles = 3;  // q_len * group <= 48
+#ifndef ASPIRE_ATTN_WAVES_PER_BLOCK
+#define ASPIRE_ATTN_WAVES_PER_BLOCK 4
+#endif
+// Waves per attention workgroup. The planner gives each group of num_kv_heads
+// consecutive waves the same pages (one wave per kv head); with 4 waves per
+// workgroup a group of 8 kv heads spans two workgroups dispatched together
+// (8-wave workgroups measured no faster and constrain occupancy).
+constexpr int kAttnWavesPerBlock = ASPIRE_ATTN_WAVES_PER_BLOCK;
 
 // Work item of the attention plan (8 x int32, read with scalar loads).
 struct WorkItem {

@@ -25,7 +25,6 @@
 namespace aspire {
 namespace {
 
-constexpr int kWavesPerBlock = 4;
 constexpr int kMinPagesPerWave = 8;
 
 struct Segment {
@@ -67,7 +66,7 @@ extern "C" int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu, in
   }
   if (waves_per_cu <= 0) waves_per_cu = 8;
   int32_t waves = num_cus * waves_per_cu;
-  waves = (waves + kWavesPerBlock - 1) / kWavesPerBlock * kWavesPerBlock;
+  waves = (waves + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock * kAttnWavesPerBlock;
   aspire_plan_layout L;
   L.num_waves = waves;
   L.max_items = 4 * waves + 8192;

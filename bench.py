@@ -67,6 +67,8 @@ def parse():
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-components", action="store_true",
+                    help="skip the per-component measurements (append, page list, merge, selectors, refresh layer)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (read + write) for rocprofv3 counter calibration")
     return ap.parse_args()
@@ -214,6 +216,10 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    components = None
+    if args.config == 1 and not args.no_components:
+        components = measure_components(step, w, out, args.steps, plan_us)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = run_cpu_baseline(step, args.cpu_seconds)
@@ -264,8 +270,134 @@ def main():
             "bytes_per_launch": attn_bytes,
         },
         "cpu_baseline": cpu,
+        "components": components,
     }
     print(json.dumps(line), flush=True)
+
+
+def _gbs(nbytes, us):
+    return round(nbytes / (us * 1e-6) / 1e9, 1)
+
+
+def measure_components(step, w, out, steps, plan_us):
+    """Per-row measurements beside the layer: every piece of the path, timed on its own.
+
+    Each entry: average microseconds per call (HIP events, current stream),
+    algorithmic bytes and the resulting GB/s with its fraction of 8 TB/s.
+    """
+    import ctypes
+
+    from aspire_amd import _lib
+    from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
+    from aspire_amd.attention.page_list import build_unified_indices
+    from aspire_amd.backends.page_selector import KeyMeanPageSelector, PageSelectorFirstLastAvg
+    from aspire_amd.workloads import PAGE, config2
+
+    dev = step.q.device
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+
+    def entry(us, nbytes, **extra):
+        d = {"us": round(us, 2), "bytes": int(nbytes), "gbs": _gbs(nbytes, us),
+             "frac_of_peak": round(_gbs(nbytes, us) / PEAK_HBM_GBS, 4)}
+        d.update(extra)
+        return d
+
+    # (a1) KV append alone
+    app = lambda: torch.ops.mylib.update_kv_padded(step.k_new, step.v_new, step.qo_indptr, step.cache,
+                                                   step.kv_indices, step.kv_indptr, step.last_page_len, PAGE)
+    us = timed(app, steps, stream) * 1e3
+    res["append"] = entry(us, step.total_tokens * step.hkv * 128 * 2 * 2 * 2, tokens=step.total_tokens,
+                          note="latency-bound: one workgroup per token")
+
+    # (a2) mixed page list from the draft selections and the block table
+    B = step.batch
+    width = int(step.block_table.shape[1])
+    dtab = torch.zeros(B, 128, dtype=torch.int32, device=dev)
+    dn = torch.zeros(B, dtype=torch.int32, device=dev)
+    for b in range(B):
+        if step.draft_pages[b] is not None:
+            ph = step.block_table[b, torch.from_numpy(step.draft_pages[b]).to(dev)]
+            dtab[b, : ph.numel()] = ph
+            dn[b] = ph.numel()
+    vn = torch.full((B,), width, dtype=torch.int32, device=dev)
+    idx = torch.empty(B * width, dtype=torch.int32, device=dev)
+    ptr = torch.empty(B + 2, dtype=torch.int32, device=dev)
+    pl = lambda: build_unified_indices(step.mode_flags, dtab, step.block_table, dn, vn, idx, ptr, indptr_fill_to=B + 2)
+    us = timed(pl, steps, stream) * 1e3
+    entries = int(step.kv_indptr_host[B])
+    assert torch.equal(ptr, step.kv_indptr) and torch.equal(idx[:entries], step.kv_indices)
+    res["page_list"] = entry(us, entries * 8 + B * 16, entries=entries)
+
+    # (a7) host planner
+    res["plan_host"] = {"us": round(plan_us, 1), "note": "C++ planner + async upload of the live plan segments"}
+
+    # (a6) split-KV merge alone (partials from the last attention run)
+    info = w.plan_info
+    a = _lib.AttentionArgs()
+    k_cache, v_cache = step.cache[:, 0], step.cache[:, 1]
+    a.q, a.q_stride_t, a.q_stride_h = step.q.data_ptr(), step.q.stride(0), step.q.stride(1)
+    a.kv_cache, a.cache_stride_p = k_cache.data_ptr(), k_cache.stride(0)
+    a.cache_stride_kv = (v_cache.data_ptr() - k_cache.data_ptr()) // 2
+    a.cache_stride_t, a.cache_stride_h = k_cache.stride(1), k_cache.stride(2)
+    a.kv_indices = w._kv_indices.data_ptr()
+    a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.plan_dev, a.float_ws = w._int_workspace.data_ptr(), w._float_workspace.data_ptr()
+    a.num_qo_heads, a.num_kv_heads, a.head_dim, a.page_size = step.hq, step.hkv, 128, PAGE
+    a.sm_scale, a.causal, a.class_mask, a.launch_merge = 1.0 / 128 ** 0.5, 1, 0, 1
+
+    def merge():
+        _lib.check(_lib.lib().aspire_attention_run(ctypes.byref(w._layout), ctypes.byref(a), _lib.stream_of(out)),
+                   "merge")
+
+    us = timed(merge, steps, stream) * 1e3
+    merge_bytes = info.partial_rows * 129 * 4 + info.num_merge * 16 * 256
+    res["merge"] = entry(us, merge_bytes, merges=info.num_merge, partial_rows=info.partial_rows)
+
+    # refresh layer (config 2): full attention + key-mean page scores + top-128 per (row, kv head)
+    step2 = config2(device=dev)
+    w2 = HolisticAttentionWrapper(torch.empty(1, device=dev), "NHD")
+    w2.plan(step2.qo_indptr, step2.kv_indptr, step2.kv_indices, step2.last_page_len, 32, 8, 128, PAGE, causal=True)
+    out2 = torch.empty_like(step2.q)
+    max_pages = int(step2.block_table.shape[1])
+    ks = KeyMeanPageSelector(step2.batch, 8, max_pages, k=128, L=0, device=dev)
+    npg2 = torch.from_numpy((step2.ctx_len + PAGE - 1) // PAGE).to(torch.int32).to(dev)
+
+    def refresh():
+        w2.run(step2.q, step2.cache, out=out2, page_scores=ks.page_scores)
+        ks.select(npg2, step2.block_table)
+
+    for _ in range(3):
+        refresh()
+    us = timed(refresh, steps, stream) * 1e3
+    nb2 = step2.algorithmic_bytes(include_append=False)
+    sel_bytes = step2.batch * 8 * 128 * 4 * 2 + int(npg2.sum()) * 8 * 4 * 2  # scores written + read, lists out
+    res["refresh_layer_config2"] = entry(us, nb2["total"] + sel_bytes, batch=step2.batch,
+                                         kv_tokens=int(step2.kv_len_host.sum()),
+                                         note="attention with the key-mean page-score epilogue + top-128 per (row, kv head)")
+
+    # (a3) reference first/last selector at refresh-layer scale (B=64, 32 heads, 32k max context)
+    Bs, H, max_seq = step2.batch, 32, 32768
+    gen = torch.Generator(device=dev).manual_seed(7)
+    dump = (torch.randn(Bs, H, 2, max_seq, generator=gen, device=dev) * 6).to(torch.float16)
+    pos = torch.arange(max_seq, device=dev)
+    ctx = torch.from_numpy(step2.ctx_len).to(dev)
+    dump.masked_fill_(pos[None, None, None, :] >= ctx[:, None, None, None], float("-inf"))
+    lse = torch.randn(Bs * 10, H, generator=gen, device=dev) + 8
+    qo = torch.arange(Bs + 2, dtype=torch.int32, device=dev) * 4
+    table = torch.arange(Bs * 2048, dtype=torch.int32, device=dev).view(Bs, 2048)
+    sel = PageSelectorFirstLastAvg(Bs, 2048, 144, 8, H, PAGE, max_seq, dev, Bs, 9, draft_percent=7.0,
+                                   min_draft_pages=32)
+    selr = lambda: sel.select(dump.view(-1), lse, npg2, table, qo)
+    for _ in range(2):
+        selr()
+    us = timed(selr, steps, stream) * 1e3
+    dump_bytes = int(npg2.sum()) * 16 * H * 2 * 2
+    res["select_first_last"] = entry(us, dump_bytes + Bs * 2048 * 4 * 2 + Bs * 144 * 4, rows=Bs, heads=H,
+                                     note="reference (R) selector: dump read over each row's pages + top-k")
+    del dump, step2, w2
+    torch.cuda.synchronize()
+    return res
 
 
 def run_cpu_baseline(step, budget_s):
