@@ -184,6 +184,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 
   const bool do_dump = p.dump_kind != 0 && (p.dump_flags == nullptr || p.dump_flags[b] != 0);
   const bool do_score = p.page_scores != nullptr && it.q_len == 1;
+  float score_buf = 0.f;
   const int dump_slots = p.dump_kind == 2 ? 2 : 1;
 
   // Page ids are read with scalar loads (constant address space): they are
@@ -247,15 +248,24 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
           float rs = 0.f;
 #pragma unroll
           for (int i = 0; i < 4; ++i) rs += (base_pos + i < kv_len) ? s[t][i] : 0.f;
-          rs += shfl_xor_f(rs, 16);
-          rs += shfl_xor_f(rs, 32);
+          rs = add_xor32(add_xor16(rs));
           const int cnt = min(16, kv_len - pg * 16);
-          float val = (r < G) ? rs / float(cnt) : kNegInf;
-          val = fmaxf(val, shfl_xor_f(val, 1));
-          val = fmaxf(val, shfl_xor_f(val, 2));
-          val = fmaxf(val, shfl_xor_f(val, 4));
-          val = fmaxf(val, shfl_xor_f(val, 8));
-          if (lane == 0) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + pg] = val;
+          float val = (r < G) ? (cnt == 16 ? rs * 0.0625f : rs / float(cnt)) : kNegInf;
+          // max over the group's heads (lanes r < G of each row)
+          if (G > 1) val = fmaxf(val, dpp_xor1(val));
+          if (G > 2) val = fmaxf(val, dpp_xor2(val));
+          if (G > 4) val = fmaxf(val, shfl_xor_f(val, 4));
+          if (G > 8) val = fmaxf(val, shfl_xor_f(val, 8));
+          // Lane 0 holds the page's score. Lane (pg - pb) % 64 keeps it; the
+          // wave writes 64 pages at once (one coalesced store instead of a
+          // single-lane store per page, which would share vmcnt with the K/V
+          // loads in flight).
+          const int slot = (pg - pb) & 63;
+          const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val), 0));
+          score_buf = lane == slot ? v0 : score_buf;
+          if (slot == 63 || pg == pe - 1) {
+            if (lane <= slot) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + (pg - slot) + lane] = score_buf;
+          }
         }
 
         float x[4];
@@ -263,8 +273,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
         for (int i = 0; i < 4; ++i)
           x[i] = (base_pos + i <= limit[t]) ? s[t][i] * p.scale_log2 : kNegInf;
         float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-        mx = fmaxf(mx, shfl_xor_f(mx, 16));
-        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        mx = max_xor32(max_xor16(mx));
         const float m_new = fmaxf(m[t], mx);
         float a = 1.f;
         float pv[4] = {0.f, 0.f, 0.f, 0.f};

@@ -144,4 +144,46 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Cross-row reductions of a 64-lane wave without LDS. permlane32_swap(v, v)
+// returns (v[l % 32], v[l % 32 + 32]) and permlane16_swap(v, v) returns the
+// values of rows (2k, 2k + 1) of 16 lanes for both rows of that pair, so
+// combining the pair equals combining v with v[l ^ 32] (v[l ^ 16]).
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+// Sum of an int over the 64 lanes, all in VALU: DPP quad permutes (xor 1,
+// xor 2), row_half_mirror and row_mirror (they pair quad q with 1 - q and
+// half h with 1 - h once those are uniform), then the permlane swaps.
+__device__ __forceinline__ int wave_sum_int(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  const auto p16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = int(p16[0]) + int(p16[1]);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  v = int(p32[0]) + int(p32[1]);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+// v[l ^ 1] and v[l ^ 2] through DPP quad permutes ([1,0,3,2] and [2,3,0,1]).
+__device__ __forceinline__ float dpp_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
 }  // namespace aspire

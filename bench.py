@@ -86,6 +86,23 @@ def timed(fn, steps, stream):
     return start.elapsed_time(end) / steps  # ms
 
 
+def graph_timed(fn, steps, stream, reps=20, warm=2):
+    """Average device ms per call of fn: `reps` calls captured in one HIP graph,
+    replayed `steps` times (amortises the graph launch over the captured calls)."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    ms = timed(g.replay, steps, stream) / reps
+    del g
+    return ms
+
+
 def attention_only(w, q, cache, out):
     """Launch only the attention kernels of w's current plan (no merge), as run() would."""
     import ctypes
@@ -306,9 +323,9 @@ def measure_components(step, w, out, steps, plan_us):
     # (a1) KV append alone
     app = lambda: torch.ops.mylib.update_kv_padded(step.k_new, step.v_new, step.qo_indptr, step.cache,
                                                    step.kv_indices, step.kv_indptr, step.last_page_len, PAGE)
-    us = timed(app, steps, stream) * 1e3
+    us = graph_timed(app, steps, stream) * 1e3
     res["append"] = entry(us, step.total_tokens * step.hkv * 128 * 2 * 2 * 2, tokens=step.total_tokens,
-                          note="latency-bound: one workgroup per token")
+                          note="20 calls per graph replay; latency-bound: one workgroup per token")
 
     # (a2) mixed page list from the draft selections and the block table
     B = step.batch
@@ -324,10 +341,10 @@ def measure_components(step, w, out, steps, plan_us):
     idx = torch.empty(B * width, dtype=torch.int32, device=dev)
     ptr = torch.empty(B + 2, dtype=torch.int32, device=dev)
     pl = lambda: build_unified_indices(step.mode_flags, dtab, step.block_table, dn, vn, idx, ptr, indptr_fill_to=B + 2)
-    us = timed(pl, steps, stream) * 1e3
+    us = graph_timed(pl, steps, stream) * 1e3
     entries = int(step.kv_indptr_host[B])
     assert torch.equal(ptr, step.kv_indptr) and torch.equal(idx[:entries], step.kv_indices)
-    res["page_list"] = entry(us, entries * 8 + B * 16, entries=entries)
+    res["page_list"] = entry(us, entries * 8 + B * 16, entries=entries, note="20 calls per graph replay")
 
     # (a7) host planner
     res["plan_host"] = {"us": round(plan_us, 1), "note": "C++ planner + async upload of the live plan segments"}
@@ -350,9 +367,10 @@ def measure_components(step, w, out, steps, plan_us):
         _lib.check(_lib.lib().aspire_attention_run(ctypes.byref(w._layout), ctypes.byref(a), _lib.stream_of(out)),
                    "merge")
 
-    us = timed(merge, steps, stream) * 1e3
+    us = graph_timed(merge, steps, stream) * 1e3
     merge_bytes = info.partial_rows * 129 * 4 + info.num_merge * 16 * 256
-    res["merge"] = entry(us, merge_bytes, merges=info.num_merge, partial_rows=info.partial_rows)
+    res["merge"] = entry(us, merge_bytes, merges=info.num_merge, partial_rows=info.partial_rows,
+                         note="20 calls per graph replay; bytes = fp32 partials read + 16 bf16 rows out per merge")
 
     # refresh layer (config 2): full attention + key-mean page scores + top-128 per (row, kv head)
     step2 = config2(device=dev)
@@ -363,18 +381,26 @@ def measure_components(step, w, out, steps, plan_us):
     ks = KeyMeanPageSelector(step2.batch, 8, max_pages, k=128, L=0, device=dev)
     npg2 = torch.from_numpy((step2.ctx_len + PAGE - 1) // PAGE).to(torch.int32).to(dev)
 
-    def refresh():
+    def refresh_attention():
         w2.run(step2.q, step2.cache, out=out2, page_scores=ks.page_scores)
+
+    def refresh_topk():
         ks.select(npg2, step2.block_table)
 
-    for _ in range(3):
-        refresh()
-    us = timed(refresh, steps, stream) * 1e3
+    def refresh():
+        refresh_attention()
+        refresh_topk()
+
+    us = graph_timed(refresh, steps, stream) * 1e3
+    us_att = graph_timed(refresh_attention, steps, stream) * 1e3
+    us_topk = graph_timed(refresh_topk, steps, stream) * 1e3
     nb2 = step2.algorithmic_bytes(include_append=False)
     sel_bytes = step2.batch * 8 * 128 * 4 * 2 + int(npg2.sum()) * 8 * 4 * 2  # scores written + read, lists out
     res["refresh_layer_config2"] = entry(us, nb2["total"] + sel_bytes, batch=step2.batch,
                                          kv_tokens=int(step2.kv_len_host.sum()),
-                                         note="attention with the key-mean page-score epilogue + top-128 per (row, kv head)")
+                                         attention_us=round(us_att, 2), topk_us=round(us_topk, 2),
+                                         note="20 calls per graph replay: attention with the key-mean page-score epilogue"
+                                              " + top-128 per (row, kv head)")
 
     # (a3) reference first/last selector at refresh-layer scale (B=64, 32 heads, 32k max context)
     Bs, H, max_seq = step2.batch, 32, 32768
@@ -389,12 +415,10 @@ def measure_components(step, w, out, steps, plan_us):
     sel = PageSelectorFirstLastAvg(Bs, 2048, 144, 8, H, PAGE, max_seq, dev, Bs, 9, draft_percent=7.0,
                                    min_draft_pages=32)
     selr = lambda: sel.select(dump.view(-1), lse, npg2, table, qo)
-    for _ in range(2):
-        selr()
-    us = timed(selr, steps, stream) * 1e3
+    us = graph_timed(selr, steps, stream) * 1e3
     dump_bytes = int(npg2.sum()) * 16 * H * 2 * 2
     res["select_first_last"] = entry(us, dump_bytes + Bs * 2048 * 4 * 2 + Bs * 144 * 4, rows=Bs, heads=H,
-                                     note="reference (R) selector: dump read over each row's pages + top-k")
+                                     note="20 calls per graph replay; reference (R) selector: dump read over each row's pages + top-k")
     del dump, step2, w2
     torch.cuda.synchronize()
     return res

@@ -160,3 +160,98 @@ def test_keymean_selector_config2_shape(gpu):
             logical = [inv[int(p)] for p in selected[b, g, :k].cpu().numpy()]
             assert logical == sorted(logical)
             assert_topk_sets(logical, ref_scores[b * 8 + g, :n].double().numpy(), k)
+
+
+def _topk_expected(scores, n, L, kk, table_row, order):
+    """Top-kk of one segment: +inf for the last L pages, ties by lowest index, ascending logical."""
+    sc = scores[:n].astype(np.float32).copy()
+    if L > 0:
+        sc[max(n - L, 0):] = np.inf
+    u = sc.view(np.uint32).astype(np.int64)
+    key = np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+    pick = np.sort(np.argsort(-key, kind="stable")[:kk])
+    phys = table_row[pick]
+    return np.sort(phys) if order == 0 else phys
+
+
+@pytest.mark.parametrize("order", [0, 1])
+@pytest.mark.parametrize("stride", [12288, 2048, 700])
+def test_topk_kernel_exact_with_ties_and_wide_rows(gpu, order, stride):
+    """Keys in LDS (stride > 2048) and in registers (stride <= 2048); counts above the stride are clamped."""
+    say("topk exact", order, stride)
+    rng = np.random.default_rng(11 + order)
+    segs = 8
+    npg = np.array([12288, 5000, 300, 64, 1, 0, 2049, 230], dtype=np.int32)
+    # coarse values -> many exact ties; a few +-inf
+    scores = (rng.integers(-40, 40, size=(segs, stride)) * 0.25).astype(np.float32)
+    scores[1, ::97] = np.inf
+    scores[2, :50] = -np.inf
+    table = np.stack([rng.permutation(stride).astype(np.int32) for _ in range(segs)])
+    L, subset, width = 3, 1500, 1800
+    sel = torch.full((segs, width), -1, dtype=torch.int32, device=gpu)
+    valid = torch.zeros(segs, dtype=torch.int32, device=gpu)
+    sd, nd, td = (torch.from_numpy(a).to(gpu) for a in (scores, npg, table))
+    _lib.check(_lib.lib().aspire_select_topk(_lib.ptr(sd), stride, _lib.ptr(nd), None, segs, 1, L, 0, subset, 0, 0.0,
+                                             _lib.ptr(td), stride, order, _lib.ptr(sel), width, width,
+                                             _lib.ptr(valid), _lib.stream_of(sd)), "topk")
+    torch.cuda.synchronize()
+    got, got_valid = sel.cpu().numpy(), valid.cpu().numpy()
+    for s in range(segs):
+        n = min(int(npg[s]), stride)
+        k = min(n, subset)
+        assert got_valid[s] == k
+        exp = _topk_expected(scores[s], n, L, k, table[s], order)
+        assert np.array_equal(got[s, :k], exp), s
+        assert not got[s, k:].any()
+
+
+def test_topk_kernel_width_clamp_and_percent_count(gpu):
+    rng = np.random.default_rng(5)
+    segs, stride = 4, 4096
+    npg = np.array([4096, 1000, 17, 3], dtype=np.int32)
+    scores = rng.standard_normal((segs, stride)).astype(np.float32)
+    table = np.tile(np.arange(stride, dtype=np.int32), (segs, 1))
+    width, pct, lo, hi = 64, 7.0, 20, 400
+    sel = torch.full((segs, width), -1, dtype=torch.int32, device=gpu)
+    valid = torch.zeros(segs, dtype=torch.int32, device=gpu)
+    sd, nd, td = (torch.from_numpy(a).to(gpu) for a in (scores, npg, table))
+    _lib.check(_lib.lib().aspire_select_topk(_lib.ptr(sd), stride, _lib.ptr(nd), None, segs, 1, 0, 2, hi, lo, pct,
+                                             _lib.ptr(td), stride, 0, _lib.ptr(sel), width, width,
+                                             _lib.ptr(valid), _lib.stream_of(sd)), "topk")
+    torch.cuda.synchronize()
+    for s in range(segs):
+        n = int(npg[s])
+        k = min(max(int(np.ceil(np.float32(n) * np.float32(pct) / np.float32(100.0))), min(n, lo)), min(n, hi))
+        assert int(valid[s]) == k
+        kk = min(k, width)
+        assert np.array_equal(sel[s, :kk].cpu().numpy(), _topk_expected(scores[s], n, 0, kk, table[s], 0))
+
+
+def test_selectors_graph_replays_match_eager(gpu):
+    """Both selectors captured in a HIP graph (as the reference replays them): every replay equals eager."""
+    say("selector graph replays")
+    z = np.load(GOLDEN)
+    sel, inp, g = _golden_case(z, "percent", gpu, "physical")
+    eager_sel, eager_valid = (t.clone() for t in sel.select(**inp))
+    step = build_step(hq=32, hkv=8, ctx_len=[3000, 4096, 700], q_len=[1] * 3, is_draft=[0] * 3,
+                      draft_budget=0, seed=3, device=gpu)
+    npg = torch.from_numpy((step.ctx_len + 15) // 16).to(torch.int32).to(gpu)
+    ks = KeyMeanPageSelector(3, 8, int(step.block_table.shape[1]), k=64, L=2, device=gpu)
+    ks.page_scores.copy_(torch.randn(ks.page_scores.shape, generator=torch.Generator(device=gpu).manual_seed(1),
+                                     device=gpu))
+    k_sel, k_cnt = (t.clone() for t in ks.select(npg, step.block_table))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sel.select(**inp)
+        ks.select(npg, step.block_table)
+    for rep in range(3):
+        sel._selected_buf.fill_(-7)
+        ks.selected.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got_sel, got_valid = sel._selected_buf[: eager_sel.shape[0], : eager_sel.shape[1]], sel._valid_counts_buf
+        assert torch.equal(got_sel, eager_sel), rep
+        assert torch.equal(got_valid[: eager_valid.numel()], eager_valid), rep
+        assert torch.equal(ks.selected[:3], k_sel) and torch.equal(ks.counts[:3], k_cnt), rep
