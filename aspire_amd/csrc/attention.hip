@@ -38,7 +38,8 @@ struct AttnParams {
   int64_t o_st, o_sh;
   float* lse;
   const int32_t* plan;
-  int64_t indptr_off, items_off;
+  int64_t indptr_off[3], items_off[3];
+  int class_mask;
   int32_t num_waves;
   float* part_o;
   float* part_lse;
@@ -67,9 +68,6 @@ struct MergeParams {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-#ifndef ASPIRE_NT1_WAVES
-#define ASPIRE_NT1_WAVES 3
-#endif
 #ifndef ASPIRE_DIM_MAP
 #define ASPIRE_DIM_MAP 1
 #endif
@@ -400,30 +398,13 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   }
 }
 
-// Waves per SIMD the register allocation must allow: the kernel is bound by
-// bytes in flight, so occupancy is worth more than spare registers.
+// Items of one row-tile class for this wave.
 template <int NT>
-struct Occupancy {
-  static constexpr int waves = NT == 1 ? ASPIRE_NT1_WAVES : 2;
-};
-
-template <int NT>
-__global__ __launch_bounds__(64 * kAttnWavesPerBlock) __attribute__((amdgpu_waves_per_eu(Occupancy<NT>::waves)))
-void attention_kernel(AttnParams p) {
-  const int lane = threadIdx.x & 63;
-  const int wave = wave_uniform(blockIdx.x * kAttnWavesPerBlock + (threadIdx.x >> 6));
-  if (wave >= p.num_waves) return;
-  const int32_t* indptr = p.plan + p.indptr_off;
+__device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, int lane, i16x4 ident) {
+  const int32_t* indptr = p.plan + p.indptr_off[c];
   const int w0 = wave_uniform(indptr[wave]);
   const int w1 = wave_uniform(indptr[wave + 1]);
-  if (w0 >= w1) return;
-  // Identity B operand: lane holds B[k = 4*grp + j][n = r] = (k == n).
-  const int r = lane & 15, grp = lane >> 4;
-  const uint32_t one = 0x3f80u;  // bf16 1.0
-  uint32_t e0 = (4 * grp + 0 == r ? one : 0u) | ((4 * grp + 1 == r ? one : 0u) << 16);
-  uint32_t e1 = (4 * grp + 2 == r ? one : 0u) | ((4 * grp + 3 == r ? one : 0u) << 16);
-  const i16x4 ident = as_i16x4(e0, e1);
-  const WorkItem* items = reinterpret_cast<const WorkItem*>(p.plan + p.items_off);
+  const WorkItem* items = reinterpret_cast<const WorkItem*>(p.plan + p.items_off[c]);
   for (int w = w0; w < w1; ++w) {
     WorkItem it;
     it.q_start = wave_uniform(items[w].q_start);
@@ -436,6 +417,27 @@ void attention_kernel(AttnParams p) {
     it.partial_row = wave_uniform(items[w].partial_row);
     run_item<NT>(p, it, lane, ident);
   }
+}
+
+// One persistent launch for all row-tile classes: each wave runs its class-1
+// items, then class 2, then class 3 (the planner balances every class over
+// the waves), so the launch has one ramp and one tail. Registers follow the
+// 3-tile class (2 waves per SIMD), which is also what the default grid of
+// 8 waves per CU asks for.
+__global__ __launch_bounds__(64 * kAttnWavesPerBlock) __attribute__((amdgpu_waves_per_eu(2)))
+void attention_kernel(AttnParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_uniform(blockIdx.x * kAttnWavesPerBlock + (threadIdx.x >> 6));
+  if (wave >= p.num_waves) return;
+  // Identity B operand: lane holds B[k = 4*grp + j][n = r] = (k == n).
+  const int r = lane & 15, grp = lane >> 4;
+  const uint32_t one = 0x3f80u;  // bf16 1.0
+  uint32_t e0 = (4 * grp + 0 == r ? one : 0u) | ((4 * grp + 1 == r ? one : 0u) << 16);
+  uint32_t e1 = (4 * grp + 2 == r ? one : 0u) | ((4 * grp + 3 == r ? one : 0u) << 16);
+  const i16x4 ident = as_i16x4(e0, e1);
+  if (p.class_mask & 1) run_class<1>(p, 0, wave, lane, ident);
+  if (p.class_mask & 2) run_class<2>(p, 1, wave, lane, ident);
+  if (p.class_mask & 4) run_class<3>(p, 2, wave, lane, ident);
 }
 
 // Merge of split segments: one wave per (merge item, query row); lane l owns
@@ -599,15 +601,12 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((layout->num_waves + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock);
   for (int c = 0; c < 3; ++c) {
-    if (!(a->class_mask & (1 << c))) continue;
-    p.indptr_off = off.indptr[c];
-    p.items_off = off.items[c];
-    if (c == 0)
-      hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
-    else if (c == 1)
-      hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
-    else
-      hipLaunchKernelGGL(attention_kernel<3>, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
+    p.indptr_off[c] = off.indptr[c];
+    p.items_off[c] = off.items[c];
+  }
+  p.class_mask = a->class_mask & 7;
+  if (p.class_mask) {
+    hipLaunchKernelGGL(attention_kernel, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
     ASPIRE_CHECK_LAUNCH();
   }
   if (a->launch_merge) {

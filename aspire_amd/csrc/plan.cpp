@@ -160,6 +160,11 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
   int64_t partial_rows = 0;
   int64_t total_pages = 0;
   int num_items[3] = {0, 0, 0};
+  // One kernel launch runs every class (each wave takes its class-1 items,
+  // then class 2, then class 3), so a class using fewer slots than there are
+  // starts where the previous class's slots ended: small classes land on
+  // different waves instead of all on the first ones.
+  int64_t rot = 0;
 
   for (int c = 0; c < 3; ++c) {
     const auto& segs = sc.segs[c];
@@ -178,7 +183,7 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
       int zero_rr = 0;
       for (const auto& s : segs) {
         if (s.npages == 0) {
-          const int64_t slot = zero_rr++ % s_eff;
+          const int64_t slot = (zero_rr++ % s_eff + rot) % slots;
           for (int gg = 0; gg < hpu; ++gg) {
             WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, 0, 0, s.bg + gg, -1};
             sc.items.emplace_back(static_cast<int32_t>(slot * hpu + gg), it);
@@ -205,7 +210,7 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
             const int64_t prow = pieces > 1 ? first + (int64_t(gg) * pieces + k) * s.rows : -1;
             WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, static_cast<int32_t>(wb - a),
                         static_cast<int32_t>(we - a), s.bg + gg, static_cast<int32_t>(prow)};
-            sc.items.emplace_back(static_cast<int32_t>(j * hpu + gg), it);
+            sc.items.emplace_back(static_cast<int32_t>(((j + rot) % slots) * hpu + gg), it);
           }
         }
         if (pieces > 1)
@@ -224,6 +229,7 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
       sc.merges.resize(merges_before);
       s_eff = std::max<int64_t>(1, s_eff / 2);
     }
+    if (!segs.empty()) rot = (rot + s_eff) % slots;
     if (static_cast<int64_t>(sc.items.size()) > L.max_items) {
       set_error("aspire_plan_build: class %d needs %zu work items, capacity %d", c,
                 sc.items.size(), L.max_items);

@@ -9,7 +9,10 @@ Shapes follow BASELINE.json's configs (page size 16, head_dim 128, bf16):
   tokens, a 65536-page pool in random order; rows 0-15 draft (q_len 1 over 128
   selected pages), rows 16-31 verify (q_len 4);
 * config 2 - Qwen3-8B refresh layer: batch 64, contexts uniform in
-  [8192, 32768], every row a single query over its full cache.
+  [8192, 32768], every row a single query over its full cache;
+* config 4 - DeepSeek-R1-Distill-Llama-8B shape (32 / 8 heads), batch 16,
+  contexts uniform in [65536, 131072]; a fraction f of the rows draft (q_len 1
+  over a 256-page selection), the rest verify with q_len uniform in {2..9}.
 
 K, V and Q are N(0, 1); every (page, kv head) adds one N(0, 0.5^2) scalar to
 all 16 of its keys so page scores separate. A row's context length is its KV
@@ -183,4 +186,18 @@ def config2(device="cpu", seed=0, batch: int = 64, lo: int = 8192, hi: int = 327
     rng = np.random.default_rng(seed + 1000)
     ctx = rng.integers(lo, hi + 1, size=batch)
     return build_step(hq=32, hkv=8, ctx_len=ctx, q_len=[1] * batch, is_draft=[0] * batch, draft_budget=0,
+                      seed=seed, device=device)
+
+
+def config4(device="cpu", seed=0, draft_frac: float = 0.0, batch: int = 16, lo: int = 65536,
+            hi: int = 131072, draft_budget: int = 256) -> MixedStep:
+    """Long-context layer: batch 16, contexts U[65536, 131072]; round(f * batch) seeded draft rows
+    (q_len 1 over draft_budget pages), the others verify with q_len U{2..9}."""
+    rng = np.random.default_rng(seed + 4000)
+    ctx = rng.integers(lo, hi + 1, size=batch)
+    n_draft = int(round(draft_frac * batch))
+    is_draft = np.zeros(batch, dtype=bool)
+    is_draft[rng.permutation(batch)[:n_draft]] = True
+    q_len = np.where(is_draft, 1, rng.integers(2, 10, size=batch))
+    return build_step(hq=32, hkv=8, ctx_len=ctx, q_len=q_len, is_draft=is_draft, draft_budget=draft_budget,
                       seed=seed, device=device)

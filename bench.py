@@ -103,8 +103,9 @@ def graph_timed(fn, steps, stream, reps=20, warm=2):
     return ms
 
 
-def attention_only(w, q, cache, out):
-    """Launch only the attention kernels of w's current plan (no merge), as run() would."""
+def attention_only(w, q, cache, out, class_mask=None):
+    """Launch only the attention kernels of w's current plan (no merge), as run() would;
+    ``class_mask`` limits the launch to some row-tile classes."""
     import ctypes
 
     from aspire_amd import _lib
@@ -124,6 +125,8 @@ def attention_only(w, q, cache, out):
     a.sm_scale, a.causal = 1.0 / 128 ** 0.5, 1
     info = w.plan_info
     a.class_mask = sum(1 << c for c in range(3) if info.num_items[c] > 0)
+    if class_mask is not None:
+        a.class_mask &= class_mask
     a.launch_merge = 0
     layout = w._layout
 
@@ -236,6 +239,7 @@ def main():
     components = None
     if args.config == 1 and not args.no_components:
         components = measure_components(step, w, out, args.steps, plan_us)
+        components["long_context_config4"] = measure_config4(args.steps, args.waves_per_cu)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -421,6 +425,52 @@ def measure_components(step, w, out, steps, plan_us):
                                      note="20 calls per graph replay; reference (R) selector: dump read over each row's pages + top-k")
     del dump, step2, w2
     torch.cuda.synchronize()
+    return res
+
+
+def measure_config4(steps, waves_per_cu, fracs=(0.0, 0.25, 0.5, 0.75, 1.0)):
+    """Config 4 (batch 16, contexts U[64k, 128k], verify q_len U{2..9}, 256-page drafts):
+    attention + split-KV merge per draft fraction f, timed eagerly like the main step."""
+    from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
+    from aspire_amd.workloads import PAGE, config4
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for f in fracs:
+        st = config4(device=dev, draft_frac=f)
+        w = HolisticAttentionWrapper(torch.empty(1, device=dev), "NHD", waves_per_cu=waves_per_cu)
+        w.plan(st.qo_indptr, st.kv_indptr, st.kv_indices, st.last_page_len, st.hq, st.hkv, 128, PAGE, causal=True)
+        out = torch.empty_like(st.q)
+        fn = lambda: w.run(st.q, st.cache, out=out)
+        for _ in range(3):
+            fn()
+        ms = timed(fn, steps, stream)
+        nb = st.algorithmic_bytes(include_append=False)["total"]
+        info = w.plan_info
+        gbs = nb / (ms * 1e-3) / 1e9
+        # each row-tile class alone (rows = q_len * group: <=16, <=32, <=48)
+        rows = st.q_len * (st.hq // st.hkv)
+        cls = np.where(rows <= 16, 0, np.where(rows <= 32, 1, 2))
+        kvl = st.kv_len_host.numpy()[: st.batch].astype(np.int64)
+        per_class = {}
+        for c in range(3):
+            if info.num_items[c] == 0:
+                continue
+            fn_c = attention_only(w, st.q, st.cache, out, class_mask=1 << c)
+            fn_c()
+            us_c = timed(fn_c, steps, stream) * 1e3
+            nb_c = int(kvl[cls == c].sum()) * st.hkv * 128 * 4
+            per_class[f"class{c + 1}"] = {"us": round(us_c, 1), "kv_bytes": nb_c,
+                                          "gbs": round(nb_c / (us_c * 1e-6) / 1e9, 1)}
+        res[f"f={f}"] = {"us": round(ms * 1e3, 1), "bytes": nb, "gbs": round(gbs, 1),
+                         "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "draft_rows": int(st.is_draft.sum()),
+                         "q_len": st.q_len.tolist(), "items_per_class": list(info.num_items),
+                         "merges": info.num_merge, "partial_rows": info.partial_rows, "per_class": per_class}
+        log(f"config4 f={f}: {ms * 1e3:.1f} us -> {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%}), "
+            f"items {list(info.num_items)}, merges {info.num_merge}; per class {per_class}")
+        del st, w, out
+        torch.cuda.empty_cache()
     return res
 
 
