@@ -71,11 +71,13 @@ constexpr float kNegInf = -__builtin_huge_valf();
 #ifndef ASPIRE_DIM_MAP
 #define ASPIRE_DIM_MAP 1
 #endif
-#ifndef ASPIRE_NT_LOADS
-#define ASPIRE_NT_LOADS 0
+// The 1-tile class streams K/V with non-temporal loads (measured slightly
+// faster for it, and slower for the 2- and 3-tile classes).
+#ifndef ASPIRE_NT1_NTLOADS
+#define ASPIRE_NT1_NTLOADS 1
 #endif
-#ifndef ASPIRE_PIPE
-#define ASPIRE_PIPE 0
+#ifndef ASPIRE_ATTN_WAVES_PER_EU
+#define ASPIRE_ATTN_WAVES_PER_EU 2
 #endif
 
 // Element offset of the 8-dim slice c (0..3) a lane of group grp owns. Any
@@ -88,14 +90,7 @@ __device__ __forceinline__ int dim_off(int grp, int c) {
 
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 
-__device__ __forceinline__ uint4 load16(const uint16_t* ptr) {
-#if ASPIRE_NT_LOADS
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
-  return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return *reinterpret_cast<const uint4*>(ptr);
-#endif
-}
+__device__ __forceinline__ uint4 load16(const uint16_t* ptr) { return *reinterpret_cast<const uint4*>(ptr); }
 
 // K / V loads go through buffer resources: a per-page scalar descriptor (base =
 // the page's K or V rows of this kv head) and one per-lane 32-bit byte offset
@@ -109,10 +104,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint16_t* base
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, bytes, kBufferConfig);
 }
 
+// NTL sets the non-temporal policy bit (aux 2): streamed K/V is read once.
+template <bool NTL>
 __device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rsrc, int voff, uint4 (&dst)[4]) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + 64 * c, 0, ASPIRE_NT_LOADS ? 2 : 0);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + 64 * c, 0, NTL ? 2 : 0);
     dst[c] = make_uint4(v.x, v.y, v.z, v.w);
   }
 }
@@ -138,6 +135,7 @@ __device__ __forceinline__ void store_dump(const AttnParams& p, int64_t idx, flo
 template <int NT>
 __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it, int lane,
                                          i16x4 ident) {
+  constexpr bool kNtl = NT == 1 && ASPIRE_NT1_NTLOADS;
   const int r = lane & 15;
   const int grp = lane >> 4;
   const int G = p.group;
@@ -200,11 +198,11 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   const int lane_off = (r * int(p.c_st) + 8 * grp) * 2;
   const int rows_bytes = (15 * int(p.c_st) + kHeadDim) * 2;
   auto load_k = [&](int64_t phys, bool ok, uint4(&dst)[4]) {
-    load_rows(page_rsrc(p.cache + phys * p.c_sp + int64_t(g) * p.c_sh, rows_bytes), ok ? lane_off : kOutOfRange,
+    load_rows<kNtl>(page_rsrc(p.cache + phys * p.c_sp + int64_t(g) * p.c_sh, rows_bytes), ok ? lane_off : kOutOfRange,
               dst);
   };
   auto load_v = [&](int64_t phys, bool ok, uint4(&dst)[4]) {
-    load_rows(page_rsrc(p.cache + phys * p.c_sp + p.c_skv + int64_t(g) * p.c_sh, rows_bytes),
+    load_rows<kNtl>(page_rsrc(p.cache + phys * p.c_sp + p.c_skv + int64_t(g) * p.c_sh, rows_bytes),
               ok ? lane_off : kOutOfRange, dst);
   };
 
@@ -286,6 +284,19 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
         pf[t] = as_i16x4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]));
       }
 
+      // Rescale the accumulators only when some row's running max moved: once
+      // the max settles (most pages), alpha is exactly 1 for every row and the
+      // multiplies are skipped (a wave-uniform branch; results are unchanged).
+      bool moved = false;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) moved |= alpha[t] != 1.f;
+      if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[t][j] *= alpha[t];
+      }
+
       // O^T += V^T P^T, one 16-dim slice at a time: transpose the slice with an
       // exact identity MFMA (the values are bf16 already), then accumulate.
 #pragma unroll
@@ -295,17 +306,16 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
         const f32x4 d = mfma_16x16x16_bf16(va, ident, f32x4{0.f, 0.f, 0.f, 0.f});
         const i16x4 vt = as_i16x4(pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3]));
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][j] = mfma_16x16x16_bf16(vt, pf[t], acc[t][j] * alpha[t]);
+        for (int t = 0; t < NT; ++t) acc[t][j] = mfma_16x16x16_bf16(vt, pf[t], acc[t][j]);
       }
       after_pv();
   };
 
-#if ASPIRE_PIPE == 0
   // One K/V register buffer pipelined at half-page granularity: the next
   // page's K is requested as soon as this page's QK^T has consumed K, and its V
   // as soon as P.V has consumed each V slice (about one page in flight per
-  // wave, 32 VGPRs). Prologue and loop share one block so the loop head sees a
-  // single, straight-line load order.
+  // wave, 32 VGPRs; a second buffer measured no faster). Prologue and loop
+  // share one block so the loop head sees a single, straight-line load order.
   if (pb < pe) {
     uint4 kr[4], vr[4];
     {
@@ -327,35 +337,6 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       page_body(pg, kr, vr, [&] { load_k(next_phys, next_ok, kr); }, [&] { load_v(next_phys, next_ok, vr); });
     } while (++pg < pe);
   }
-#else
-  auto nothing = [] {};
-  // Two K/V register buffers: the next page's K and V are requested before the
-  // current page is computed (up to two pages in flight, 64 VGPRs).
-  uint4 ka[4], va[4], kb[4], vb[4];
-  if (pb < pe) {
-    const int64_t phys = page_id(pb);
-    const bool ok = pb * 16 + r < kv_len;
-    load_k(phys, ok, ka);
-    load_v(phys, ok, va);
-  }
-  for (int pg = pb; pg < pe; pg += 2) {
-    if (pg + 1 < pe) {
-      const int64_t phys = page_id(pg + 1);
-      const bool ok = (pg + 1) * 16 + r < kv_len;
-      load_k(phys, ok, kb);
-      load_v(phys, ok, vb);
-    }
-    page_body(pg, ka, va, nothing, nothing);
-    if (pg + 1 >= pe) break;
-    if (pg + 2 < pe) {
-      const int64_t phys = page_id(pg + 2);
-      const bool ok = (pg + 2) * 16 + r < kv_len;
-      load_k(phys, ok, ka);
-      load_v(phys, ok, va);
-    }
-    page_body(pg + 1, kb, vb, nothing, nothing);
-  }
-#endif
 
   // Epilogue: normalise and write the final output or the fp32 partial.
 #pragma unroll
@@ -422,10 +403,10 @@ __device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, 
 // One persistent launch for all row-tile classes: each wave runs its class-1
 // items, then class 2, then class 3 (the planner balances every class over
 // the waves), so the launch has one ramp and one tail. Registers follow the
-// 3-tile class (2 waves per SIMD), which is also what the default grid of
-// 8 waves per CU asks for.
-__global__ __launch_bounds__(64 * kAttnWavesPerBlock) __attribute__((amdgpu_waves_per_eu(2)))
-void attention_kernel(AttnParams p) {
+// 3-tile class (at most 2 waves per SIMD); the default grid runs one wave per
+// SIMD.
+__global__ __launch_bounds__(64 * kAttnWavesPerBlock)
+__attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_kernel(AttnParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(blockIdx.x * kAttnWavesPerBlock + (threadIdx.x >> 6));
   if (wave >= p.num_waves) return;

@@ -64,7 +64,10 @@ extern "C" int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu, in
     num_cus = cached_cu_count();
     if (num_cus <= 0) return fail(ASPIRE_ERR_HIP, "aspire_plan_layout_init: cannot query CU count");
   }
-  if (waves_per_cu <= 0) waves_per_cu = 8;
+  // One wave per SIMD: measured best on MI355X for every row-tile mix (with
+  // more waves per CU they contend for HBM and the long wide-row workloads
+  // lose up to 10%).
+  if (waves_per_cu <= 0) waves_per_cu = 4;
   int32_t waves = num_cus * waves_per_cu;
   waves = (waves + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock * kAttnWavesPerBlock;
   aspire_plan_layout L;

@@ -126,7 +126,7 @@ typedef struct aspire_plan_info {
   int64_t live_bytes;         /* bytes the upload copies */
 } aspire_plan_info;
 
-/* num_cus <= 0 queries the current device. waves_per_cu <= 0 uses 8. */
+/* num_cus <= 0 queries the current device. waves_per_cu <= 0 uses 4 (one wave per SIMD). */
 int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu,
                             int64_t int_ws_bytes, int64_t float_ws_bytes,
                             int32_t head_dim, aspire_plan_layout* out);
