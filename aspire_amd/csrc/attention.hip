@@ -53,6 +53,7 @@ struct AttnParams {
   const int32_t* dump_flags;
   float* page_scores;
   int64_t ps_stride;
+  int32_t staged_ok;  // cache layout allows workgroup-staged K/V (see run_item)
 };
 
 struct MergeParams {
@@ -79,6 +80,25 @@ constexpr float kNegInf = -__builtin_huge_valf();
 #ifndef ASPIRE_ATTN_WAVES_PER_EU
 #define ASPIRE_ATTN_WAVES_PER_EU 2
 #endif
+#ifndef ASPIRE_STAGED
+#define ASPIRE_STAGED 1
+#endif
+
+// Workgroup-staged K/V (1-tile items of head-aligned plans): LDS per workgroup,
+// two buffers x {K, V} x 16 key rows x 1 KiB (the rows' 4 heads), in uint4.
+constexpr int kStageRowChunks = 64;                      // 16-byte chunks per 1 KiB row-half
+constexpr int kStageKv = 16 * kStageRowChunks;           // one of K / V
+constexpr int kStageBuf = 2 * kStageKv;                  // one buffer
+constexpr int kStageChunks = 2 * kStageBuf;              // 64 KiB
+static_assert(kAttnWavesPerBlock == 4, "staged K/V assumes 4-wave workgroups (4 kv heads)");
+
+// LDS-only release/acquire around the workgroup barrier: waits for this
+// wave's LDS writes (lgkmcnt) but not for its K/V loads in flight.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // Element offset of the 8-dim slice c (0..3) a lane of group grp owns. Any
 // assignment works as long as K, V, Q and the output agree (the MFMA sums over
@@ -134,7 +154,7 @@ __device__ __forceinline__ void store_dump(const AttnParams& p, int64_t idx, flo
 
 template <int NT>
 __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it, int lane,
-                                         i16x4 ident) {
+                                         i16x4 ident, bool staged, uint4* stage_lds) {
   constexpr bool kNtl = NT == 1 && ASPIRE_NT1_NTLOADS;
   const int r = lane & 15;
   const int grp = lane >> 4;
@@ -311,12 +331,84 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       after_pv();
   };
 
+  if constexpr (NT == 1) {
+    if (staged) {
+      // Workgroup-staged K/V. The workgroup's 4 waves hold kv heads g0..g0+3
+      // of one head-aligned slot: the same pages, and together 1 KiB of
+      // contiguous cache per key row (the rows' 4 heads). Wave wl loads 8 of the
+      // page's 32 row-halves (K or V, key rows 8*(wl&1)..+7) as whole 1 KiB
+      // rows, one 128-bit non-temporal load per lane and row, and stores them to
+      // LDS; after a barrier every wave reads its own head's rows from LDS in the
+      // MFMA operand layout. Contiguous 1 KiB loads stream measurably faster
+      // from HBM than 16 rows x 64 B per instruction. LDS chunk c of key row r
+      // sits at c ^ r, so the row writes and the 16-row column reads both hit 16
+      // different bank groups. Two LDS buffers: page pg is read from one while
+      // page pg + 1 is stored to the other and page pg + 2 is in flight.
+      if (pb < pe) {
+        const int wl = (threadIdx.x >> 6) & 3;
+        const int kvh = wl >> 1, r0 = (wl & 1) * 8;
+        const int g0 = g & ~3, gl = g & 3;
+        const int row_b = int(p.c_st) * 2;
+        const int span = int(p.c_skv) * 2 + 15 * row_b + 4 * kHeadDim * 2;
+        const int st_off = kvh * int(p.c_skv) * 2 + r0 * row_b + lane * 16;
+        auto stage_load = [&](int64_t phys, bool ok, uint4(&st)[8]) {
+          const __amdgpu_buffer_rsrc_t rs = page_rsrc(p.cache + phys * p.c_sp + int64_t(g0) * p.c_sh, span);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? st_off + i * row_b : kOutOfRange, 0, 2);
+            st[i] = make_uint4(v.x, v.y, v.z, v.w);
+          }
+        };
+        auto stage_store = [&](int buf, const uint4(&st)[8]) {
+          uint4* base = stage_lds + buf * kStageBuf + kvh * kStageKv;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int row = r0 + i;
+            base[row * kStageRowChunks + (lane ^ row)] = st[i];
+          }
+        };
+        auto read_rows = [&](int buf, int kv, uint4(&dst)[4]) {
+          const uint4* base = stage_lds + buf * kStageBuf + kv * kStageKv + r * kStageRowChunks;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) dst[c] = base[(gl * 16 + c * 4 + grp) ^ r];
+        };
+        uint4 st[8];
+        stage_load(page_id(pb), true, st);
+        stage_store(0, st);
+        stage_load(page_id(pb + 1), pb + 1 < pe, st);
+        stage_barrier();
+        int64_t id_ahead = page_id(pb + 2);
+        int pg = pb;
+        do {
+          const int buf = (pg - pb) & 1;
+          uint4 kr[4], vr[4];
+          read_rows(buf, 0, kr);
+          const bool v_ok = pg * 16 + r < kv_len;  // rows past kv_len may hold stale values
+          page_body(
+              pg, kr, vr,
+              [&] {
+                read_rows(buf, 1, vr);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) vr[c] = v_ok ? vr[c] : make_uint4(0, 0, 0, 0);
+              },
+              [&] {
+                stage_store(buf ^ 1, st);
+                const int64_t nphys = id_ahead;
+                id_ahead = page_id(pg + 3);
+                stage_load(nphys, pg + 2 < pe, st);
+                stage_barrier();
+              });
+        } while (++pg < pe);
+      }
+    }
+  }
+
   // One K/V register buffer pipelined at half-page granularity: the next
   // page's K is requested as soon as this page's QK^T has consumed K, and its V
   // as soon as P.V has consumed each V slice (about one page in flight per
   // wave, 32 VGPRs; a second buffer measured no faster). Prologue and loop
   // share one block so the loop head sees a single, straight-line load order.
-  if (pb < pe) {
+  if (!(NT == 1 && staged) && pb < pe) {
     uint4 kr[4], vr[4];
     {
       const int64_t phys = page_id(pb);
@@ -381,7 +473,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 
 // Items of one row-tile class for this wave.
 template <int NT>
-__device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, int lane, i16x4 ident) {
+__device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, int lane, i16x4 ident,
+                                          bool staged, uint4* stage_lds) {
   const int32_t* indptr = p.plan + p.indptr_off[c];
   const int w0 = wave_uniform(indptr[wave]);
   const int w1 = wave_uniform(indptr[wave + 1]);
@@ -396,7 +489,7 @@ __device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, 
     it.page_end = wave_uniform(items[w].page_end);
     it.bg = wave_uniform(items[w].bg);
     it.partial_row = wave_uniform(items[w].partial_row);
-    run_item<NT>(p, it, lane, ident);
+    run_item<NT>(p, it, lane, ident, staged, stage_lds);
   }
 }
 
@@ -416,9 +509,16 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
   uint32_t e0 = (4 * grp + 0 == r ? one : 0u) | ((4 * grp + 1 == r ? one : 0u) << 16);
   uint32_t e1 = (4 * grp + 2 == r ? one : 0u) | ((4 * grp + 3 == r ? one : 0u) << 16);
   const i16x4 ident = as_i16x4(e0, e1);
-  if (p.class_mask & 1) run_class<1>(p, 0, wave, lane, ident);
-  if (p.class_mask & 2) run_class<2>(p, 1, wave, lane, ident);
-  if (p.class_mask & 4) run_class<3>(p, 2, wave, lane, ident);
+  // Head-aligned plans (header[4] = kv heads per slot, a multiple of 4) give
+  // the 4 waves of a workgroup the same pages: their 1-tile items stage K/V
+  // through LDS. The flag is uniform over the workgroup, so every wave takes
+  // the same barriers.
+  __shared__ uint4 stage_lds[kStageChunks];
+  const int hpu = wave_uniform(p.plan[4]);
+  const bool staged = p.staged_ok && hpu > 0 && hpu % 4 == 0;
+  if (p.class_mask & 1) run_class<1>(p, 0, wave, lane, ident, staged, stage_lds);
+  if (p.class_mask & 2) run_class<2>(p, 1, wave, lane, ident, staged, stage_lds);
+  if (p.class_mask & 4) run_class<3>(p, 2, wave, lane, ident, staged, stage_lds);
 }
 
 // Merge of split segments: one wave per (merge item, query row); lane l owns
@@ -579,6 +679,10 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
   p.dump_flags = a->dump_mode_flags;
   p.page_scores = a->page_scores;
   p.ps_stride = a->page_score_stride;
+  // Staged K/V reads 4 adjacent heads as one 1 KiB row; byte offsets within a
+  // page (both kv halves, 16 rows) must fit the 32-bit buffer offsets.
+  p.staged_ok = ASPIRE_STAGED && a->cache_stride_h == kHeadDim &&
+                (a->cache_stride_kv + 15 * a->cache_stride_t + 4 * kHeadDim) * 2 < (int64_t(1) << 30);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((layout->num_waves + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock);
   for (int c = 0; c < 3; ++c) {

@@ -86,7 +86,7 @@ struct MergeItem {
 
 // Fixed offsets (int32 units) of the plan in the int workspace.
 struct PlanOffsets {
-  int64_t header;        // [0]=items c0, [1]=c1, [2]=c2, [3]=num_merge
+  int64_t header;        // [0]=items c0, [1]=c1, [2]=c2, [3]=num_merge, [4]=kv heads per slot
   int64_t indptr[3];     // num_waves + 1 entries each
   int64_t items[3];      // max_items WorkItems each
   int64_t merge;         // max_merge MergeItems

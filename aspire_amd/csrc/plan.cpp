@@ -259,6 +259,7 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
   buf[off.header + 1] = num_items[1];
   buf[off.header + 2] = num_items[2];
   buf[off.header + 3] = static_cast<int32_t>(sc.merges.size());
+  buf[off.header + 4] = hpu;  // kv heads per slot (waves of a slot share pages)
 
   info->num_items[0] = num_items[0];
   info->num_items[1] = num_items[1];
