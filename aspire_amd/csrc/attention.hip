@@ -83,6 +83,12 @@ constexpr float kNegInf = -__builtin_huge_valf();
 #ifndef ASPIRE_STAGED
 #define ASPIRE_STAGED 1
 #endif
+// Row-tile classes (1..3) whose items use the staged path. The 3-tile class
+// keeps direct loads: its query fragments and accumulators leave no registers
+// for the staging buffer (it spills, and measured slower).
+#ifndef ASPIRE_STAGED_MAX_NT
+#define ASPIRE_STAGED_MAX_NT 2
+#endif
 
 // Workgroup-staged K/V (1-tile items of head-aligned plans): LDS per workgroup,
 // two buffers x {K, V} x 16 key rows x 1 KiB (the rows' 4 heads), in uint4.
@@ -331,7 +337,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       after_pv();
   };
 
-  if constexpr (NT == 1) {
+  if constexpr (NT <= ASPIRE_STAGED_MAX_NT) {
     if (staged) {
       // Workgroup-staged K/V. The workgroup's 4 waves hold kv heads g0..g0+3
       // of one head-aligned slot: the same pages, and together 1 KiB of
@@ -408,7 +414,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   // as soon as P.V has consumed each V slice (about one page in flight per
   // wave, 32 VGPRs; a second buffer measured no faster). Prologue and loop
   // share one block so the loop head sees a single, straight-line load order.
-  if (!(NT == 1 && staged) && pb < pe) {
+  if (!(NT <= ASPIRE_STAGED_MAX_NT && staged) && pb < pe) {
     uint4 kr[4], vr[4];
     {
       const int64_t phys = page_id(pb);
