@@ -3,26 +3,24 @@
 // One wave processes one (row, kv head) segment piece at a time: all
 // q_len * group query rows of the GQA group against a contiguous range of
 // the segment's 16-token pages. Per page and lane (r = lane % 16 selects a
-// key / query row, grp = lane / 16 a 32-dim slice):
-//   * K and V: lane reads 64 contiguous bytes (4 x 128-bit loads each) of key
-//     r, dims [32*grp, 32*grp + 32): one wave instruction covers 16 rows x
-//     64 B, four cover the page-head's 4 KB;
+// key / query row, grp = lane / 16 a group of 8-dim slices):
+//   * K and V reach the lane as 4 x 128 bits of key r: dims 32c + 8grp
+//     (c = 0..3), either staged through LDS by the workgroup (head-aligned
+//     plans: 1 KiB contiguous row loads, see run_item) or loaded directly
+//     (16 rows x 64 B per instruction);
 //   * S^T = K . Q^T with 4 v_mfma_f32_16x16x32_bf16 (A = K rows straight from
 //     registers, B = the row's Q slice; the MFMA sums over k in any order both
-//     operands agree on, so the 64-byte lane slice needs no shuffle). Lane
-//     holds S^T[key 4*grp + i][row r], which is already the B operand layout
-//     of the P.V product;
+//     operands agree on, so the lane slices need no shuffle). Lane holds
+//     S^T[key 4*grp + i][row r], which is already the B operand layout of the
+//     P.V product;
 //   * V is transposed in registers by an exact MFMA against the identity
 //     (8 x v_mfma_f32_16x16x16_bf16): lane then holds V[keys 4*grp..+3][dim]
 //     as the A operand of O^T = V^T . P^T, and the O^T accumulator of lane l
-//     covers row r, dims 32*grp + 4*vt + i -- its own contiguous 64 B of
-//     output;
+//     covers row r and its own 32 output dims;
 //   * online softmax in fp32 with exp2 and a base-2 LSE; the row max is
-//     reduced across the 4 lane groups with two xor shuffles.
-// No LDS is used. K/V stream through one 32-VGPR register buffer pipelined at
-// half-page granularity (the next page's K is requested once QK^T has consumed
-// K, its V once P.V has consumed V). A row tile is 16 query rows; NT tiles
-// share the K/V registers (q_len * group <= 16 * NT).
+//     reduced across the 4 lane groups with permlane swaps (no LDS).
+// A row tile is 16 query rows; NT tiles share the K/V registers
+// (q_len * group <= 16 * NT). One persistent launch runs every class.
 #include "common.h"
 
 namespace aspire {

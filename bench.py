@@ -61,8 +61,8 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=1, choices=[1, 2])
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -238,8 +238,8 @@ def main():
 
     components = None
     if args.config == 1 and not args.no_components:
-        components = measure_components(step, w, out, args.steps, plan_us)
-        components["long_context_config4"] = measure_config4(args.steps, args.waves_per_cu)
+        components = measure_components(step, w, out, min(args.steps, 50), plan_us)
+        components["long_context_config4"] = measure_config4(min(args.steps, 100), args.waves_per_cu)
 
     cpu = None
     if not args.no_cpu_baseline:
