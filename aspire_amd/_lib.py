@@ -33,6 +33,8 @@ EXPORTED = (
     "aspire_merge_states",
     "aspire_select_first_last_scores",
     "aspire_select_topk",
+    "aspire_host_plan_reset",
+    "aspire_host_plan_step",
 )
 
 
@@ -83,6 +85,39 @@ class AttentionArgs(ctypes.Structure):
 
 
 _lock = threading.Lock()
+class HostPlanConfig(ctypes.Structure):
+    _fields_ = [
+        ("page_size", ctypes.c_int32), ("max_batch", ctypes.c_int32), ("draft_kind", ctypes.c_int32),
+        ("full_kind", ctypes.c_int32), ("subset_cache_size", ctypes.c_int32), ("table_width", ctypes.c_int32),
+        ("min_draft_pages", ctypes.c_int32), ("draft_percent", ctypes.c_float), ("valid_floor_l", ctypes.c_int32),
+        ("pages_per_slot", ctypes.c_int32),
+    ]
+
+
+class HostPlanStateC(ctypes.Structure):
+    _fields_ = [("draft_num_pages", ctypes.c_void_p), ("prev_verify", ctypes.c_void_p)]
+
+
+class HostPlanInputs(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("verify", ctypes.c_void_p), ("finished", ctypes.c_void_p),
+        ("draft_counts", ctypes.c_void_p), ("seq_lens", ctypes.c_void_p), ("total_tokens", ctypes.c_int64),
+        ("bucket_tokens", ctypes.c_int64),
+    ]
+
+
+class HostPlanOutputs(ctypes.Structure):
+    _fields_ = [
+        ("qo_indptr", ctypes.c_void_p), ("kv_indptr", ctypes.c_void_p), ("kv_len", ctypes.c_void_p),
+        ("full_kv_indptr", ctypes.c_void_p), ("full_kv_len", ctypes.c_void_p), ("dec", ctypes.c_void_p),
+        ("verify_num_pages", ctypes.c_void_p), ("effective_num_pages", ctypes.c_void_p),
+        ("last_page_len", ctypes.c_void_p), ("input_pos", ctypes.c_void_p), ("sample_indices", ctypes.c_void_p),
+        ("position_indices", ctypes.c_void_p), ("token_capacity", ctypes.c_int64),
+        ("refresh_rows", ctypes.c_void_p), ("spill_rows", ctypes.c_void_p), ("n_refresh", ctypes.c_int32),
+        ("n_spill", ctypes.c_int32),
+    ]
+
+
 _lib = None
 
 
@@ -105,6 +140,9 @@ def _declare(lib):
                                             i32, vp],  # ..., scores, score_stride, slots, stream
         "aspire_select_topk": [vp, i64, vp, vp, i32, i32, i32, i32, i32, i32, f32, vp, i64, i32, vp, i64, i32,
                                vp, vp],
+        "aspire_host_plan_reset": [ctypes.POINTER(HostPlanConfig), vp, vp, vp, vp, i32],
+        "aspire_host_plan_step": [ctypes.POINTER(HostPlanConfig), ctypes.POINTER(HostPlanStateC),
+                                  ctypes.POINTER(HostPlanInputs), ctypes.POINTER(HostPlanOutputs)],
     }
     for name, argtypes in sigs.items():
         fn = getattr(lib, name)

@@ -350,8 +350,26 @@ def measure_components(step, w, out, steps, plan_us):
     assert torch.equal(ptr, step.kv_indptr) and torch.equal(idx[:entries], step.kv_indices)
     res["page_list"] = entry(us, entries * 8 + B * 16, entries=entries, note="20 calls per graph replay")
 
-    # (a7) host planner
+    # (a7) host planner, and the native host mirror that renders its input arrays each step
     res["plan_host"] = {"us": round(plan_us, 1), "note": "C++ planner + async upload of the live plan segments"}
+    from aspire_amd.backends.host_plan import HostPlanConfig, HostPlanState
+    hp = HostPlanState(HostPlanConfig(page_size=PAGE, max_batch=step.batch, draft_kind="replan",
+                                      full_kind="effective_full", subset_cache_size=128, table_width=2048,
+                                      min_draft_pages=None, draft_percent=None, valid_floor_l=8,
+                                      pages_per_slot=2048))
+    seq = np.asarray(step.ctx_len, dtype=np.int64) - step.q_len
+    hp.reset_all(seq)
+    ver = ~np.asarray(step.is_draft, dtype=bool)
+    fin = np.zeros(step.batch, dtype=bool)
+    dcnt = np.where(ver, step.q_len - 1, 0).astype(np.int64)
+    tot = int(np.where(ver, dcnt + 1, 1).sum())
+    reps = 2000
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        hp.build_step(verify=ver, finished=fin, draft_counts=dcnt, seq_lens=seq, total_tokens=tot,
+                      bucket_tokens=tot)
+    res["host_plan_step"] = {"us": round((time.perf_counter() - t0) / reps * 1e6, 2), "rows": step.batch,
+                             "note": "HostPlanState.build_step (native mirror) per decode step, host only"}
 
     # (a6) split-KV merge alone (partials from the last attention run)
     info = w.plan_info

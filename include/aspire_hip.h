@@ -226,6 +226,89 @@ int aspire_select_topk(const float* scores, int64_t score_stride, const int32_t*
                        int32_t order, int32_t* selected, int64_t sel_stride,
                        int32_t sel_width, int32_t* valid, void* stream);
 
+/* ------------------------------------------------------------------ host plan
+ * Native host mirror of the per-step plan arrays. Replaces HostPlanState
+ * (aspire/backends/host_plan.py:30-306): HostPlanConfig becomes
+ * aspire_host_plan_config, reset_all / reset_slots become
+ * aspire_host_plan_reset, build_step becomes aspire_host_plan_step. Host
+ * memory only; no device work and no synchronisation. */
+enum {
+  ASPIRE_DRAFT_REPLAN = 0,      /* 'replan' (host_plan.py:38-39) */
+  ASPIRE_DRAFT_SINK_RECENT = 1, /* 'sink_recent' */
+  ASPIRE_DRAFT_GATED = 2,       /* 'gated' */
+  ASPIRE_FULL_NONE = 0,         /* full_kind None: no dump wrapper */
+  ASPIRE_FULL_MIRROR = 1,       /* 'mirror': dump wrapper reuses the mixed arrays */
+  ASPIRE_FULL_EFFECTIVE = 2     /* 'effective_full' */
+};
+
+typedef struct aspire_host_plan_config {
+  int32_t page_size;
+  int32_t max_batch;
+  int32_t draft_kind;        /* ASPIRE_DRAFT_* */
+  int32_t full_kind;         /* ASPIRE_FULL_* */
+  int32_t subset_cache_size;
+  int32_t table_width;
+  int32_t min_draft_pages;   /* < 0: None */
+  float draft_percent;       /* < 0: None (evaluated in fp32, as the device does) */
+  int32_t valid_floor_l;
+  int32_t pages_per_slot;    /* > 0: static arange index layout for 'effective_full' */
+} aspire_host_plan_config;
+
+/* Mirror state, caller-owned: max_batch entries each. */
+typedef struct aspire_host_plan_state {
+  int64_t* draft_num_pages;
+  uint8_t* prev_verify;
+} aspire_host_plan_state;
+
+/* Pre-step row state from the scheduler (build_step's keyword arguments). */
+typedef struct aspire_host_plan_inputs {
+  int32_t batch;               /* rows this step (<= max_batch) */
+  const uint8_t* verify;       /* [batch] */
+  const uint8_t* finished;     /* [batch] */
+  const int64_t* draft_counts; /* [batch] */
+  const int64_t* seq_lens;     /* [batch] */
+  int64_t total_tokens;
+  int64_t bucket_tokens;
+} aspire_host_plan_inputs;
+
+/* Rendered arrays. qo_indptr / kv_indptr / full_kv_indptr hold max_batch + 2
+ * entries and kv_len / full_kv_len max_batch + 1 (padding rows filled as the
+ * reference does); per-row arrays hold batch entries; refresh_rows / spill_rows
+ * (optional) hold up to max_batch; sample_indices / position_indices
+ * (optional) up to token_capacity. */
+typedef struct aspire_host_plan_outputs {
+  int32_t* qo_indptr;
+  int32_t* kv_indptr;
+  int32_t* kv_len;
+  int32_t* full_kv_indptr;     /* 'effective_full' only */
+  int32_t* full_kv_len;        /* 'effective_full' only */
+  int64_t* dec;
+  int64_t* verify_num_pages;
+  int64_t* effective_num_pages;
+  int64_t* last_page_len;
+  int64_t* input_pos;
+  int64_t* sample_indices;
+  int64_t* position_indices;
+  int64_t token_capacity;
+  int64_t* refresh_rows;
+  int64_t* spill_rows;
+  int32_t n_refresh;           /* written */
+  int32_t n_spill;             /* written */
+} aspire_host_plan_outputs;
+
+/* reset_all (slot_ids == NULL: rows 0..n-1, every verify flag cleared) or
+ * reset_slots (host_plan.py:138-151): seeds draft_num_pages from each row's
+ * page count. */
+int aspire_host_plan_reset(const aspire_host_plan_config* cfg, int64_t* draft_num_pages,
+                           uint8_t* prev_verify, const int64_t* slot_ids,
+                           const int64_t* seq_lens, int32_t n);
+
+/* build_step (host_plan.py:155-306): advances the state by one step and
+ * renders the arrays. ASPIRE_ERR_INVALID (state left as the reference leaves
+ * it) when the token total disagrees with the scheduler's. */
+int aspire_host_plan_step(const aspire_host_plan_config* cfg, aspire_host_plan_state* state,
+                          const aspire_host_plan_inputs* in, aspire_host_plan_outputs* out);
+
 #ifdef __cplusplus
 }
 #endif
