@@ -35,6 +35,8 @@ EXPORTED = (
     "aspire_select_topk",
     "aspire_host_plan_reset",
     "aspire_host_plan_step",
+    "aspire_qk_norm_rope_append",
+    "aspire_rope_frequencies",
 )
 
 
@@ -118,6 +120,26 @@ class HostPlanOutputs(ctypes.Structure):
     ]
 
 
+class RopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_stride_t", ctypes.c_int64), ("q_stride_h", ctypes.c_int64),
+        ("num_qo_heads", ctypes.c_int32),
+        ("k", ctypes.c_void_p), ("k_stride_t", ctypes.c_int64), ("k_stride_h", ctypes.c_int64),
+        ("num_kv_heads", ctypes.c_int32),
+        ("v", ctypes.c_void_p), ("v_stride_t", ctypes.c_int64), ("v_stride_h", ctypes.c_int64),
+        ("total_tokens", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("q_norm_weight", ctypes.c_void_p), ("k_norm_weight", ctypes.c_void_p), ("norm_eps", ctypes.c_float),
+        ("permute", ctypes.c_int32), ("rope_theta", ctypes.c_float), ("rope_scale", ctypes.c_float),
+        ("llama31", ctypes.c_int32), ("low_freq_factor", ctypes.c_float), ("high_freq_factor", ctypes.c_float),
+        ("old_context_len", ctypes.c_float),
+        ("indptr", ctypes.c_void_p), ("offsets", ctypes.c_void_p), ("num_rows", ctypes.c_int32),
+        ("kv_cache", ctypes.c_void_p), ("cache_stride_p", ctypes.c_int64), ("cache_stride_kv", ctypes.c_int64),
+        ("cache_stride_t", ctypes.c_int64), ("cache_stride_h", ctypes.c_int64), ("page_size", ctypes.c_int32),
+        ("kv_page_indices", ctypes.c_void_p), ("kv_page_indptr", ctypes.c_void_p),
+        ("kv_last_page_len", ctypes.c_void_p), ("num_seq", ctypes.c_int32), ("write_k", ctypes.c_int32),
+    ]
+
+
 _lib = None
 
 
@@ -143,6 +165,8 @@ def _declare(lib):
         "aspire_host_plan_reset": [ctypes.POINTER(HostPlanConfig), vp, vp, vp, vp, i32],
         "aspire_host_plan_step": [ctypes.POINTER(HostPlanConfig), ctypes.POINTER(HostPlanStateC),
                                   ctypes.POINTER(HostPlanInputs), ctypes.POINTER(HostPlanOutputs)],
+        "aspire_qk_norm_rope_append": [ctypes.POINTER(RopeArgs), vp],
+        "aspire_rope_frequencies": [i32, f32, f32, i32, f32, f32, f32, vp],
     }
     for name, argtypes in sigs.items():
         fn = getattr(lib, name)

@@ -24,40 +24,12 @@ struct AppendParams {
   int32_t page_size;
 };
 
-// Resolve token -> (row, position); returns false when the reference skips it.
-__device__ __forceinline__ bool locate(const AppendParams& p, int tok, int& row, int& pos) {
-  // Last row b in [0, num_seq) with append_indptr[b] <= tok (indptr is
-  // non-decreasing, so an empty row never shadows the row that owns tok).
-  int lo = 0, hi = p.num_seq - 1, b = -1;
-  while (lo <= hi) {
-    int mid = (lo + hi) >> 1;
-    if (p.append_indptr[mid] <= tok) {
-      b = mid;
-      lo = mid + 1;
-    } else {
-      hi = mid - 1;
-    }
-  }
-  if (b < 0) return false;
-  const int end = p.append_indptr[b + 1];
-  if (tok >= end) return false;  // covered by no row: default position -1
-  const int start_page = p.kv_indptr[b];
-  const int page_count = p.kv_indptr[b + 1] - start_page;
-  const int last = p.last_page_len[b];
-  const int seq_len = max(page_count - 1, 0) * p.page_size + last;
-  const int ps = tok + seq_len - end;
-  if (ps < 0 || page_count == 0) return false;
-  if (ps >= (page_count - 1) * p.page_size + last) return false;
-  row = start_page + ps / p.page_size;  // index into kv_indices
-  pos = ps % p.page_size;
-  return true;
-}
-
 template <bool kVec>
 __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
   const int tok = blockIdx.x;
   int list_idx, slot;
-  if (!locate(p, tok, list_idx, slot)) return;
+  if (!append_locate(p.append_indptr, p.num_seq, p.kv_indptr, p.last_page_len, p.page_size, tok, list_idx, slot))
+    return;
   const int64_t phys = p.kv_indices[list_idx];
   uint16_t* dst_k = p.cache + phys * p.c_sp + int64_t(slot) * p.c_st;
   uint16_t* dst_v = dst_k + p.c_skv;

@@ -21,7 +21,8 @@ HERE = Path(__file__).resolve().parent
 PKG = HERE.parent
 LIB = PKG / "libaspire_hip.so"
 BUILD = HERE / "_build"
-SOURCES = ["capi.cpp", "plan.cpp", "host_plan.cpp", "append.hip", "page_list.hip", "attention.hip", "select.hip"]
+SOURCES = ["capi.cpp", "plan.cpp", "host_plan.cpp", "append.hip", "page_list.hip", "attention.hip", "select.hip",
+           "rope_append.hip"]
 ARCH = "gfx950"
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function"]

@@ -178,6 +178,52 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   v = int(p32[0]) + int(p32[1]);
   return __builtin_amdgcn_readfirstlane(v);
 }
+// Sum of a float over the 64 lanes (same DPP / permlane steps as wave_sum_int).
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  return add_xor32(add_xor16(v));
+}
+
+// Paged append position of token tok (FlashInfer get_seq_lens +
+// get_batch_indices_positions, restated): the last row b with
+// append_indptr[b] <= tok owns it; with seq_len the row's cached tokens after
+// the append, the token sits at ps = tok + seq_len - append_indptr[b + 1].
+// Writes the page-list entry (kv_indptr[b] + ps / page) and the slot; false
+// when the reference skips the token (no row, negative position, empty row,
+// or past the row's length).
+__device__ __forceinline__ bool append_locate(const int32_t* append_indptr, int num_seq, const int32_t* kv_indptr,
+                                              const int32_t* last_page_len, int page_size, int tok, int& entry,
+                                              int& slot) {
+  // last b in [0, num_seq) with append_indptr[b] <= tok (indptr is
+  // non-decreasing, so an empty row never shadows the row that owns tok)
+  int lo = 0, hi = num_seq - 1, b = -1;
+  while (lo <= hi) {
+    const int mid = (lo + hi) >> 1;
+    if (append_indptr[mid] <= tok) {
+      b = mid;
+      lo = mid + 1;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  if (b < 0) return false;
+  const int end = append_indptr[b + 1];
+  if (tok >= end) return false;  // covered by no row: default position -1
+  const int start_page = kv_indptr[b];
+  const int page_count = kv_indptr[b + 1] - start_page;
+  const int last = last_page_len[b];
+  const int seq_len = max(page_count - 1, 0) * page_size + last;
+  const int ps = tok + seq_len - end;
+  if (ps < 0 || page_count == 0) return false;
+  if (ps >= (page_count - 1) * page_size + last) return false;
+  entry = start_page + ps / page_size;
+  slot = ps % page_size;
+  return true;
+}
+
 // v[l ^ 1] and v[l ^ 2] through DPP quad permutes ([1,0,3,2] and [2,3,0,1]).
 __device__ __forceinline__ float dpp_xor1(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));

@@ -331,6 +331,43 @@ def measure_components(step, w, out, steps, plan_us):
     res["append"] = entry(us, step.total_tokens * step.hkv * 128 * 2 * 2 * 2, tokens=step.total_tokens,
                           note="20 calls per graph replay; latency-bound: one workgroup per token")
 
+    # (f2) q/k RMSNorm + rotary permute + RoPE + append in one launch, against the same
+    # sequence run as the reference runs it (torch norm and permute, then rope, then append)
+    from aspire_amd.attention.rope import RopeConfig, apply_rope_inplace, qk_norm_rope_update_kv
+    gq = torch.Generator(device=dev).manual_seed(5)
+    T = step.total_tokens
+    q0 = torch.randn(T, step.hq, 128, generator=gq, device=dev).to(torch.bfloat16)
+    k0 = torch.randn(T, step.hkv, 128, generator=gq, device=dev).to(torch.bfloat16)
+    wq = torch.rand(128, generator=gq, device=dev).to(torch.bfloat16) + 0.5
+    wk = torch.rand(128, generator=gq, device=dev).to(torch.bfloat16) + 0.5
+    offs = torch.from_numpy(np.append(step.ctx_len - step.q_len, 0).astype(np.int32)).to(dev)
+    qb, kb = q0.clone(), k0.clone()
+    rc = RopeConfig(1e6)
+
+    def fused():
+        qk_norm_rope_update_kv(qb, k0, step.v_new, wq, wk, 1e-6, step.qo_indptr, offs, step.cache, step.kv_indices,
+                               step.kv_indptr, step.last_page_len, PAGE, config=rc)
+
+    def norm(x, w):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * w
+
+    def perm(x):
+        return x.view(*x.shape[:-1], 2, 64).transpose(-2, -1).reshape(x.shape)
+
+    def unfused():
+        qn, kn = perm(norm(q0, wq)), perm(norm(k0, wk))
+        apply_rope_inplace(qn, kn, step.qo_indptr, offs, rc)
+        torch.ops.mylib.update_kv_padded(kn, step.v_new, step.qo_indptr, step.cache, step.kv_indices,
+                                         step.kv_indptr, step.last_page_len, PAGE)
+
+    us_f = graph_timed(fused, steps, stream) * 1e3
+    us_u = graph_timed(unfused, steps, stream) * 1e3
+    nb = T * (step.hq * 2 + step.hkv * 2 + step.hkv * 2) * 256
+    res["qk_norm_rope_append"] = entry(us_f, nb, unfused_us=round(us_u, 2), tokens=T,
+                                       note="20 calls per graph replay; q/k RMSNorm + permute + RoPE (theta 1e6) + "
+                                            "K/V append in one launch; unfused_us: torch norm/permute + rope + append")
+
     # (a2) mixed page list from the draft selections and the block table
     B = step.batch
     width = int(step.block_table.shape[1])

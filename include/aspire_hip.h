@@ -309,6 +309,55 @@ int aspire_host_plan_reset(const aspire_host_plan_config* cfg, int64_t* draft_nu
 int aspire_host_plan_step(const aspire_host_plan_config* cfg, aspire_host_plan_state* state,
                           const aspire_host_plan_inputs* in, aspire_host_plan_outputs* out);
 
+/* ------------------------------------------------------ qk norm + rope + append
+ * One launch for the per-layer q / k preparation of the mixed forward
+ * (aspire/models/sparse_draft_transformer.py:149-171): optional q / k RMSNorm
+ * (transformer.py:505-516) with the rotary permute (transformer.py:360-364),
+ * interleaved RoPE (the mylib::rope op, mixed_transformer.py:159-198, i.e.
+ * FlashInfer apply_rope_inplace / apply_llama31_rope_inplace with
+ * interleave=True), and optionally the paged append of the rotated k and of v
+ * (mylib::update_kv_padded, kv_ops.py:127-187). q is rewritten in place; k
+ * too when write_k. Without norm weights and without a cache this is exactly
+ * mylib::rope. bf16, head_dim 128. */
+typedef struct aspire_rope_args {
+  void* q;                      /* [T, Hq, 128] bf16, in place */
+  int64_t q_stride_t, q_stride_h;
+  int32_t num_qo_heads;
+  void* k;                      /* [T, Hkv, 128] bf16 */
+  int64_t k_stride_t, k_stride_h;
+  int32_t num_kv_heads;
+  const void* v;                /* [T, Hkv, 128] bf16 (append only; may be NULL) */
+  int64_t v_stride_t, v_stride_h;
+  int32_t total_tokens;
+  int32_t head_dim;
+  const void* q_norm_weight;    /* [128] bf16, NULL: no norm (and no permute) */
+  const void* k_norm_weight;
+  float norm_eps;
+  int32_t permute;              /* permute to the interleaved layout after the norm */
+  float rope_theta, rope_scale;
+  int32_t llama31;              /* Llama 3.1 frequency smoothing */
+  float low_freq_factor, high_freq_factor, old_context_len;
+  const int32_t* indptr;        /* rows of tokens: [num_rows + 1] (the append indptr) */
+  const int32_t* offsets;       /* [num_rows] position of each row's first token */
+  int32_t num_rows;
+  void* kv_cache;               /* NULL: no append */
+  int64_t cache_stride_p, cache_stride_kv, cache_stride_t, cache_stride_h;
+  int32_t page_size;
+  const int32_t* kv_page_indices;
+  const int32_t* kv_page_indptr;
+  const int32_t* kv_last_page_len;
+  int32_t num_seq;              /* rows of the append (a prefix of the rope rows) */
+  int32_t write_k;              /* also rewrite k in place */
+} aspire_rope_args;
+
+int aspire_qk_norm_rope_append(const aspire_rope_args* args, void* stream);
+
+/* The head_dim / 2 fp32 rotary frequencies the kernel uses (host only):
+ * theta^(-2i/head_dim) / rope_scale, or the Llama 3.1 smoothing. */
+int aspire_rope_frequencies(int32_t head_dim, float rope_theta, float rope_scale, int32_t llama31,
+                            float low_freq_factor, float high_freq_factor, float old_context_len,
+                            float* out);
+
 #ifdef __cplusplus
 }
 #endif
