@@ -61,6 +61,7 @@ class PlanInfo(ctypes.Structure):
         ("max_rows", ctypes.c_int32),
         ("total_pages", ctypes.c_int64),
         ("live_bytes", ctypes.c_int64),
+        ("split_rows", ctypes.c_int32),
     ]
 
 

@@ -306,7 +306,11 @@ class HolisticAttentionWrapper:
             a.class_mask = sum(1 << c for c in range(3) if info.num_items[c] > 0)
             a.launch_merge = 1 if info.num_merge > 0 else 0
         keep_alive = [q, out, lse]
-        if self._has_jit and self._dump is not None and self._dump.kind != "noop":
+        wants_dump = self._has_jit and self._dump is not None and self._dump.kind != "noop"
+        if (wants_dump or page_scores is not None) and info.split_rows > 0:
+            raise ValueError("the logits dump and page scores need whole rows; this plan cut rows longer "
+                             "than 48 query rows into query tiles")
+        if wants_dump:
             dump_buffer = args[0]
             rest = list(args[1:])
             mode_flags = rest.pop(0) if self._dump.use_mode_flags else None

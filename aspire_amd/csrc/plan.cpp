@@ -98,7 +98,6 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
                                  int32_t num_kv_heads, int32_t page_size, int32_t causal,
                                  void* host_buf, int64_t host_buf_bytes, aspire_plan_info* info) {
   using namespace aspire;
-  (void)causal;  // the last query of a row sees every key, so the range is causal-independent
   ASPIRE_CHECK_ARG(layout && host_buf && info, "null argument");
   ASPIRE_CHECK_ARG(batch >= 0, "negative batch");
   ASPIRE_CHECK_ARG(batch == 0 || (qo_indptr && kv_indptr && kv_len), "null plan array");
@@ -128,34 +127,43 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
   const int hpu = aligned ? num_kv_heads : 1;
   int max_rows = 0;
   int num_segments = 0;
+  int split_rows = 0;
+  // A row longer than one 3-tile item (q_len * group > 48, e.g. a prefill
+  // chunk) is cut into query tiles of tile_q tokens. Each tile is planned as a
+  // row of its own whose keys end at the tile's last token: with
+  // kv_len' = kv_len - q_len + t0 + q_len', the kernel's causal limit
+  // kv_len' - q_len' + j equals the row's limit kv_len - q_len + (t0 + j), and
+  // the tile streams only the pages below it. Without the causal mask every
+  // tile sees the whole row.
+  const int tile_q = std::max(1, 16 * kMaxRowTiles / group);
   for (int b = 0; b < batch; ++b) {
     const int q_len = qo_indptr[b + 1] - qo_indptr[b];
     if (q_len <= 0) continue;
-    const int rows = q_len * group;
-    if (rows > 16 * kMaxRowTiles) {
-      set_error("aspire_plan_build: row %d has q_len %d; q_len * group must be <= %d", b, q_len,
-                16 * kMaxRowTiles);
-      return ASPIRE_ERR_INVALID;
-    }
-    max_rows = std::max(max_rows, rows);
-    const int cls = (rows - 1) / 16;
-    for (int g = 0; g < num_kv_heads; g += hpu) {
-      const int s = per_head_lists ? b * num_kv_heads + g : b;
-      const int kvl = kv_len[s];
-      const int list_pages = kv_indptr[s + 1] - kv_indptr[s];
-      if (kvl < 0 || list_pages < 0) {
-        set_error("aspire_plan_build: segment %d has negative length", s);
-        return ASPIRE_ERR_INVALID;
+    if (q_len * group > 16 * kMaxRowTiles) ++split_rows;
+    for (int t0 = 0; t0 < q_len; t0 += tile_q) {
+      const int tq = std::min(tile_q, q_len - t0);
+      const int rows = tq * group;
+      max_rows = std::max(max_rows, rows);
+      const int cls = (rows - 1) / 16;
+      for (int g = 0; g < num_kv_heads; g += hpu) {
+        const int s = per_head_lists ? b * num_kv_heads + g : b;
+        const int kvl_row = kv_len[s];
+        const int list_pages = kv_indptr[s + 1] - kv_indptr[s];
+        if (kvl_row < 0 || list_pages < 0) {
+          set_error("aspire_plan_build: segment %d has negative length", s);
+          return ASPIRE_ERR_INVALID;
+        }
+        const int kvl = causal && tq < q_len ? std::max(kvl_row - q_len + t0 + tq, 0) : kvl_row;
+        const int np = (kvl + kPage - 1) / kPage;
+        if (np > list_pages) {
+          set_error("aspire_plan_build: segment %d needs %d pages but its list holds %d", s, np,
+                    list_pages);
+          return ASPIRE_ERR_INVALID;
+        }
+        sc.segs[cls].push_back(
+            Segment{qo_indptr[b] + t0, tq, kvl, kv_indptr[s], np, (b << 8) | g, rows});
+        num_segments += hpu;
       }
-      const int np = (kvl + kPage - 1) / kPage;
-      if (np > list_pages) {
-        set_error("aspire_plan_build: segment %d needs %d pages but its list holds %d", s, np,
-                  list_pages);
-        return ASPIRE_ERR_INVALID;
-      }
-      sc.segs[cls].push_back(
-          Segment{qo_indptr[b], q_len, kvl, kv_indptr[s], np, (b << 8) | g, rows});
-      num_segments += hpu;
     }
   }
 
@@ -268,6 +276,7 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
   info->partial_rows = partial_rows;
   info->num_segments = num_segments;
   info->max_rows = max_rows;
+  info->split_rows = split_rows;
   info->total_pages = total_pages;
   info->live_bytes = (off.items[0] + int64_t(num_items[0] + num_items[1] + num_items[2]) * 8 +
                       int64_t(sc.merges.size()) * 8) *

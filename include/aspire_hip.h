@@ -124,6 +124,7 @@ typedef struct aspire_plan_info {
   int32_t max_rows;           /* largest q_len * group of any segment */
   int64_t total_pages;        /* page-heads the plan streams */
   int64_t live_bytes;         /* bytes the upload copies */
+  int32_t split_rows;         /* rows cut into query tiles (q_len * group > 48): no logits dump */
 } aspire_plan_info;
 
 /* num_cus <= 0 queries the current device. waves_per_cu <= 0 uses 4 (one wave per SIMD). */
@@ -135,8 +136,10 @@ int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu,
  * arrays). per_head_lists == 0: kv_indptr has batch+1 entries and kv_len batch
  * entries (one page list per row, shared by its kv heads); otherwise
  * batch*num_kv_heads+1 and batch*num_kv_heads, one list per (row, kv head),
- * segment index b*num_kv_heads + g. q_len * (num_qo_heads / num_kv_heads)
- * must be <= 48. */
+ * segment index b*num_kv_heads + g. A row with q_len * group > 48 (a prefill
+ * chunk; group = num_qo_heads / num_kv_heads) is cut into query tiles of
+ * 48 / group tokens, each streaming only the keys up to its last token when
+ * causal (replaces BatchPrefillWithPagedKVCacheWrapper's plan as well). */
 int aspire_plan_build(const aspire_plan_layout* layout, const int32_t* qo_indptr,
                       const int32_t* kv_indptr, const int32_t* kv_len, int32_t batch,
                       int32_t per_head_lists, int32_t num_qo_heads,

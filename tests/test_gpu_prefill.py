@@ -1,0 +1,44 @@
+"""Chunked prefill through the paged path (BatchPrefillWithPagedKVCacheWrapper drop-in) against the oracle."""
+
+import pytest
+import torch
+
+from aspire_amd.attention.holistic_wrapper import build_holistic_dump_jit_args
+from aspire_amd.attention.prefill import BatchPrefillWithPagedKVCacheWrapper
+from aspire_amd.workloads import PAGE, build_step
+from helpers import attn_close, say
+from oracle.attention import paged_attention
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_chunked_prefill_matches_oracle(gpu, causal):
+    """Prompt chunks over cached prefixes (as encode_slots plans them): 300 new tokens over 700 cached,
+    a 1000-token first chunk, 64 over 4000, and a decode row, Qwen3-8B heads (GQA 4)."""
+    say("prefill", causal)
+    step = build_step(hq=32, hkv=8, ctx_len=[1000, 1000, 4064, 5000], q_len=[300, 1000, 64, 1],
+                      is_draft=[0, 0, 0, 0], draft_budget=0, seed=31, device=gpu)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD")
+    w.plan(qo_indptr=step.qo_indptr, paged_kv_indptr=step.kv_indptr, paged_kv_indices=step.kv_indices,
+           paged_kv_last_page_len=step.last_page_len, num_qo_heads=32, num_kv_heads=8, head_dim_qk=128,
+           page_size=PAGE, q_data_type=torch.bfloat16, causal=causal)
+    assert w.plan_info.split_rows == 3
+    out, lse = w.run(step.q, step.cache, return_lse=True)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host,
+                                       step.kv_indices.cpu(), step.kv_len_host, num_kv_heads=8, causal=causal)
+    T = step.total_tokens
+    attn_close(out[:T], ref_out[:T])
+    assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
+
+
+def test_dump_refuses_split_rows(gpu):
+    step = build_step(hq=16, hkv=8, ctx_len=[200], q_len=[100], is_draft=[0], draft_budget=0, seed=2, device=gpu)
+    args = build_holistic_dump_jit_args(torch.bfloat16, 128, dump_kind="first_last_compact",
+                                        dump_buffer_dtype=torch.float16)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD", jit_args=args)
+    w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, 16, 8, 128, PAGE, causal=True)
+    dump = torch.zeros(16 * 2 * 256, dtype=torch.float16, device=gpu)
+    with pytest.raises(ValueError, match="whole rows"):
+        w.run(step.q, step.cache, dump, 16, 256)

@@ -37,7 +37,7 @@ def offsets(lay):
     return indptr, items, cur
 
 
-def plan(lay, qo, kvp, kvl, hq, hkv, per_head=False):
+def plan(lay, qo, kvp, kvl, hq, hkv, per_head=False, causal=True):
     buf = np.zeros(8 << 18, dtype=np.int32)
     info = _lib.PlanInfo()
     qo = np.ascontiguousarray(qo, dtype=np.int32)
@@ -46,7 +46,7 @@ def plan(lay, qo, kvp, kvl, hq, hkv, per_head=False):
     batch = len(kvl) // hkv if per_head else len(kvl)
     rc = _lib.lib().aspire_plan_build(
         ctypes.byref(lay), qo.ctypes.data_as(ctypes.c_void_p), kvp.ctypes.data_as(ctypes.c_void_p),
-        kvl.ctypes.data_as(ctypes.c_void_p), batch, int(per_head), hq, hkv, 16, 1,
+        kvl.ctypes.data_as(ctypes.c_void_p), batch, int(per_head), hq, hkv, 16, int(causal),
         buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, ctypes.byref(info))
     _lib.check(rc, "plan")
     return buf, info
@@ -64,7 +64,17 @@ def decode(lay, buf, info):
     return classes, merges
 
 
-def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False):
+def expected_tiles(q_len, kv_len, group, causal=True):
+    """Query tiles of a row, (t0, tq, keys): rows longer than 48 query rows are cut into
+    tiles of 48 // group tokens whose keys end at their last token (causal)."""
+    tile = max(1, 48 // group)
+    if q_len * group <= 48:
+        return [(0, q_len, kv_len)]
+    return [(t0, min(tile, q_len - t0), max(kv_len - q_len + t0 + min(tile, q_len - t0), 0) if causal else kv_len)
+            for t0 in range(0, q_len, tile)]
+
+
+def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False, causal=True):
     classes, merges = decode(lay, buf, info)
     group = hq // hkv
     seen = {}
@@ -77,26 +87,29 @@ def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False):
                 b, g = bg >> 8, bg & 255
                 assert (q_len * group - 1) // 16 == c
                 seg = b * hkv + g if per_head else b
-                assert q_start == qo[b] and q_len == qo[b + 1] - qo[b]
-                assert kv_len == kvl[seg] and base == kvp[seg]
+                tiles = {t0: (tq, keys) for t0, tq, keys in
+                         expected_tiles(qo[b + 1] - qo[b], kvl[seg], group, causal)}
+                t0 = q_start - qo[b]
+                assert t0 in tiles and (q_len, kv_len) == tiles[t0], (b, t0, q_len, kv_len)
+                assert base == kvp[seg] and pe <= (kv_len + 15) // 16
                 for p in range(pb, pe):
-                    key = (b, g, p)
+                    key = (b, g, t0, p)
                     assert key not in seen, f"page {key} planned twice"
                     seen[key] = prow
                 if prow >= 0:
                     for r in range(q_len * group):
                         assert prow + r not in partial_rows
                         partial_rows.add(prow + r)
-    # every page of every segment with queries is covered exactly once
-    for b in range(len(qo) - 1 if not per_head else len(kvl) // hkv):
-        if b >= (len(kvl) // hkv if per_head else len(kvl)):
-            break
+    # every page of every query tile of every segment with queries is covered exactly once
+    nrows = len(kvl) // hkv if per_head else len(kvl)
+    for b in range(min(len(qo) - 1, nrows)):
         if qo[b + 1] - qo[b] <= 0:
             continue
         for g in range(hkv):
             seg = b * hkv + g if per_head else b
-            for p in range((kvl[seg] + 15) // 16):
-                assert (b, g, p) in seen
+            for t0, tq, keys in expected_tiles(qo[b + 1] - qo[b], kvl[seg], group, causal):
+                for p in range((keys + 15) // 16):
+                    assert (b, g, t0, p) in seen
     # merge items reference the split pieces
     for m in merges:
         q_start, q_len, bg, first, pieces, rows = m[:6].tolist()
@@ -154,8 +167,6 @@ def test_per_head_lists():
 
 def test_rejects_bad_inputs():
     lay = layout(num_cus=4, waves_per_cu=4)
-    with pytest.raises(ValueError, match="q_len"):
-        plan(lay, np.array([0, 13]), np.array([0, 1]), np.array([16]), 32, 8)  # 13 * 4 > 48 rows
     with pytest.raises(ValueError, match="pages"):
         plan(lay, np.array([0, 1]), np.array([0, 1]), np.array([40]), 32, 8)  # list shorter than kv_len
     with pytest.raises(ValueError, match="multiple"):
@@ -172,3 +183,21 @@ def test_partial_capacity_shrinks_split():
     buf, info = plan(small, qo, kvp, kvl, hq, hkv)
     assert info.partial_rows <= small.partial_rows_cap
     check_cover(small, buf, info, qo, kvp, kvl, hq, hkv)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_rows_split_into_query_tiles(causal):
+    """Chunked prefill: rows of 300 and 1000 new tokens over prefixes of 700 and 0 tokens (GQA 4:
+    tiles of 12 tokens), beside a decode row."""
+    hq, hkv = 32, 8
+    qo = np.array([0, 300, 1300, 1301])
+    kvl = np.array([1000, 1000, 5000])
+    pages = (kvl + 15) // 16
+    kvp = np.concatenate([[0], np.cumsum(pages)])
+    lay = layout(num_cus=16, waves_per_cu=4)
+    buf, info = plan(lay, qo, kvp, kvl, hq, hkv, causal=causal)
+    assert info.split_rows == 2 and info.max_rows == 48
+    check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, causal=causal)
+    # the first tile of the second row only needs the keys up to its 12th token
+    if causal:
+        assert expected_tiles(1000, 1000, 4)[0] == (0, 12, 12)
