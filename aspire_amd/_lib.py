@@ -37,6 +37,11 @@ EXPORTED = (
     "aspire_host_plan_step",
     "aspire_qk_norm_rope_append",
     "aspire_rope_frequencies",
+    "aspire_build_head_page_lists",
+    "aspire_plan_build_segments",
+    "aspire_add_rms_norm",
+    "aspire_silu_mul",
+    "aspire_argmax_rows",
 )
 
 
@@ -168,6 +173,13 @@ def _declare(lib):
                                   ctypes.POINTER(HostPlanInputs), ctypes.POINTER(HostPlanOutputs)],
         "aspire_qk_norm_rope_append": [ctypes.POINTER(RopeArgs), vp],
         "aspire_rope_frequencies": [i32, f32, f32, i32, f32, f32, f32, vp],
+        "aspire_build_head_page_lists": [vp, i32, vp, i64, vp, vp, i64, i64, vp, i32, i32, i32, vp, i64, vp, i32,
+                                         vp],
+        "aspire_plan_build_segments": [ctypes.POINTER(PlanLayout), vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64,
+                                       ctypes.POINTER(PlanInfo)],
+        "aspire_add_rms_norm": [vp, i64, vp, i64, vp, vp, i64, i32, i32, f32, vp],
+        "aspire_silu_mul": [vp, i64, vp, i64, i32, i32, vp],
+        "aspire_argmax_rows": [vp, i64, i32, i32, vp, vp],
     }
     for name, argtypes in sigs.items():
         fn = getattr(lib, name)

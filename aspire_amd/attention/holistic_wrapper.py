@@ -180,22 +180,61 @@ class HolisticAttentionWrapper:
                              num_kv_heads, head_dim_qk, page_size, head_dim_vo, causal, sm_scale,
                              per_head_lists=per_head_lists)
 
+    def plan_segments(
+        self,
+        qo_indptr_host: torch.Tensor,
+        seg_start_host: torch.Tensor,
+        seg_pages_host: torch.Tensor,
+        seg_kv_len_host: torch.Tensor,
+        paged_kv_indices: torch.Tensor,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim_qk: int,
+        page_size: int,
+        head_dim_vo: Optional[int] = None,
+        causal: bool = False,
+        sm_scale: Optional[float] = None,
+    ) -> None:
+        """Plan per-(row, kv head) segments given by explicit list starts (not in the
+        reference): segment ``b*H_kv + g`` streams ``seg_kv_len[s]`` tokens of the
+        ``seg_pages[s]`` entries at ``paged_kv_indices[seg_start[s]]``. Rows whose
+        heads share one start (verify rows over their block table) keep the
+        row-list kernel path; rows with a list per head (the key-mean selection)
+        read each head's own pages. Same preconditions as ``plan_host``."""
+        if not self._planned:
+            raise RuntimeError("plan_segments requires a prior plan() call to resolve the kernel module")
+        self._plan_from_host(qo_indptr_host, None, seg_kv_len_host, paged_kv_indices, num_qo_heads, num_kv_heads,
+                             head_dim_qk, page_size, head_dim_vo, causal, sm_scale, per_head_lists=True,
+                             segments=(seg_start_host, seg_pages_host))
+
     def _plan_from_host(self, qo_host, kv_indptr_host, kv_len_host, paged_kv_indices, num_qo_heads,
                         num_kv_heads, head_dim_qk, page_size, head_dim_vo, causal, sm_scale, *,
-                        per_head_lists: bool) -> None:
+                        per_head_lists: bool, segments=None) -> None:
         if head_dim_vo is None:
             head_dim_vo = head_dim_qk
         if head_dim_qk != 128 or head_dim_vo != 128:
             raise ValueError("the HIP attention kernel supports head_dim 128 only")
         qo = qo_host.to(torch.int32).contiguous()
-        kvp = kv_indptr_host.to(torch.int32).contiguous()
         kvl = kv_len_host.to(torch.int32).contiguous()
         n_seg = kvl.shape[0]
         batch = n_seg // num_kv_heads if per_head_lists else n_seg
-        if qo.shape[0] < batch + 1 or kvp.shape[0] < n_seg + 1:
-            raise ValueError("plan arrays are shorter than the batch they describe")
-        if n_seg and int(kvp[: n_seg + 1].max()) > paged_kv_indices.numel():
-            raise ValueError("paged_kv_indices is shorter than kv_indptr describes")
+        if segments is not None:
+            st = segments[0].to(torch.int32).contiguous()
+            pg = segments[1].to(torch.int32).contiguous()
+            if st.shape[0] < n_seg or pg.shape[0] < n_seg or n_seg % num_kv_heads:
+                raise ValueError("segment arrays must hold batch * num_kv_heads entries")
+            if n_seg and (int(st[:n_seg].min()) < 0 or int(pg[:n_seg].min()) < 0):
+                raise ValueError("segment starts and page counts must be non-negative")
+            if n_seg and int((st[:n_seg].long() + pg[:n_seg].long()).max()) > paged_kv_indices.numel():
+                raise ValueError("paged_kv_indices is shorter than the segments describe")
+            if qo.shape[0] < batch + 1:
+                raise ValueError("plan arrays are shorter than the batch they describe")
+        else:
+            kvp = kv_indptr_host.to(torch.int32).contiguous()
+            if qo.shape[0] < batch + 1 or kvp.shape[0] < n_seg + 1:
+                raise ValueError("plan arrays are shorter than the batch they describe")
+            if n_seg and int(kvp[: n_seg + 1].max()) > paged_kv_indices.numel():
+                raise ValueError("paged_kv_indices is shorter than kv_indptr describes")
         if int(qo[: batch + 1].min()) < 0:
             raise ValueError("qo_indptr must be non-negative")
         slot = self._pinned_slot
@@ -204,10 +243,16 @@ class HolisticAttentionWrapper:
             event.synchronize()
         info = _lib.PlanInfo()
         buf = self._pinned_ring[slot]
-        rc = _lib.lib().aspire_plan_build(
-            ctypes.byref(self._layout), _lib.ptr(qo), _lib.ptr(kvp), _lib.ptr(kvl), batch,
-            1 if per_head_lists else 0, num_qo_heads, num_kv_heads, page_size, 1 if causal else 0,
-            _lib.ptr(buf), buf.numel(), ctypes.byref(info))
+        if segments is not None:
+            rc = _lib.lib().aspire_plan_build_segments(
+                ctypes.byref(self._layout), _lib.ptr(qo), _lib.ptr(st), _lib.ptr(pg), _lib.ptr(kvl), batch,
+                num_qo_heads, num_kv_heads, page_size, 1 if causal else 0, _lib.ptr(buf), buf.numel(),
+                ctypes.byref(info))
+        else:
+            rc = _lib.lib().aspire_plan_build(
+                ctypes.byref(self._layout), _lib.ptr(qo), _lib.ptr(kvp), _lib.ptr(kvl), batch,
+                1 if per_head_lists else 0, num_qo_heads, num_kv_heads, page_size, 1 if causal else 0,
+                _lib.ptr(buf), buf.numel(), ctypes.byref(info))
         _lib.check(rc, "plan")
         stream = torch.cuda.current_stream(self._device)
         rc = _lib.lib().aspire_plan_upload(ctypes.byref(self._layout), ctypes.byref(info), _lib.ptr(buf),

@@ -486,14 +486,17 @@ __device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, 
   for (int w = w0; w < w1; ++w) {
     WorkItem it;
     it.q_start = wave_uniform(items[w].q_start);
-    it.q_len = wave_uniform(items[w].q_len);
+    const int q_len_flags = wave_uniform(items[w].q_len);
+    it.q_len = q_len_flags & (kItemDirect - 1);
     it.kv_len = wave_uniform(items[w].kv_len);
     it.list_base = wave_uniform(items[w].list_base);
     it.page_begin = wave_uniform(items[w].page_begin);
     it.page_end = wave_uniform(items[w].page_end);
     it.bg = wave_uniform(items[w].bg);
     it.partial_row = wave_uniform(items[w].partial_row);
-    run_item<NT>(p, it, lane, ident, staged, stage_lds);
+    // the flag is a property of the row, so the workgroup's 4 waves (heads of one
+    // slot, walking the same rows) all take the same path
+    run_item<NT>(p, it, lane, ident, staged && !(q_len_flags & kItemDirect), stage_lds);
   }
 }
 

@@ -63,7 +63,7 @@ constexpr int kAttnWavesPerBlock = ASPIRE_ATTN_WAVES_PER_BLOCK;
 // Work item of the attention plan (8 x int32, read with scalar loads).
 struct WorkItem {
   int32_t q_start;      // first token of the row in q / out
-  int32_t q_len;        // tokens of the row
+  int32_t q_len;        // tokens of the row (| kItemDirect)
   int32_t kv_len;       // tokens in the row's (or segment's) page list
   int32_t list_base;    // kv_indices offset where the list starts
   int32_t page_begin;   // page range [page_begin, page_end) of this piece
@@ -71,6 +71,11 @@ struct WorkItem {
   int32_t bg;           // (row << 8) | kv_head
   int32_t partial_row;  // first fp32 partial row, or -1 for a final write
 };
+
+// Set in WorkItem::q_len (above the token count) for items of a head-aligned
+// plan whose kv heads read different page lists: those items load their own
+// head's rows instead of staging shared pages through LDS.
+constexpr int32_t kItemDirect = 1 << 16;
 
 // A split (row, kv head) segment whose pieces are merged (8 x int32).
 struct MergeItem {

@@ -11,11 +11,13 @@
 // segment cut by a range boundary is split into pieces that write fp32
 // partial (o, lse) rows; a merge item per split (row, kv head) combines them.
 // This balances HBM traffic per wave exactly and creates at most two split
-// pieces per slot, unlike a fixed chunk length. With row-shared page lists a
-// slot is a group of num_kv_heads consecutive waves and a segment is a whole
-// row (wave g of the group streams kv head g of the same pages at the same
-// time); with per-(row, kv head) lists a slot is one wave and a segment one
-// (row, kv head).
+// pieces per slot, unlike a fixed chunk length. When every row's kv heads
+// attend the same number of tokens, a slot is a group of num_kv_heads
+// consecutive waves and a segment is a whole row: wave g of the group streams
+// kv head g over the same page range at the same time. Rows whose heads share
+// one list then stage the pages through LDS; rows with a list per head (the
+// key-mean selection) read their own head's rows directly (their items carry
+// kItemDirect). Otherwise a slot is one wave and a segment one (row, kv head).
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -29,10 +31,13 @@ constexpr int kMinPagesPerWave = 8;
 
 struct Segment {
   int32_t q_start, q_len, kv_len, list_base, npages, bg, rows;
+  int32_t seg0;    // segment index of kv head (bg & 255), for per-head list starts
+  int32_t direct;  // kItemDirect for rows whose heads read different lists
 };
 
 struct Scratch {
   std::vector<Segment> segs[3];
+  std::vector<int32_t> start, pages;
   std::vector<std::pair<int32_t, WorkItem>> items;
   std::vector<MergeItem> merges;
   std::vector<int32_t> counts;
@@ -92,38 +97,45 @@ extern "C" int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu, in
   return ASPIRE_OK;
 }
 
-extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t* qo_indptr,
-                                 const int32_t* kv_indptr, const int32_t* kv_len, int32_t batch,
-                                 int32_t per_head_lists, int32_t num_qo_heads,
-                                 int32_t num_kv_heads, int32_t page_size, int32_t causal,
-                                 void* host_buf, int64_t host_buf_bytes, aspire_plan_info* info) {
-  using namespace aspire;
-  ASPIRE_CHECK_ARG(layout && host_buf && info, "null argument");
-  ASPIRE_CHECK_ARG(batch >= 0, "negative batch");
-  ASPIRE_CHECK_ARG(batch == 0 || (qo_indptr && kv_indptr && kv_len), "null plan array");
-  ASPIRE_CHECK_ARG(page_size == kPage, "page_size must be 16");
-  ASPIRE_CHECK_ARG(num_kv_heads > 0 && num_kv_heads < 256, "num_kv_heads must be in [1, 255]");
-  ASPIRE_CHECK_ARG(num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,
-                   "num_qo_heads must be a multiple of num_kv_heads");
-  ASPIRE_CHECK_ARG(batch < (1 << 23), "batch too large");
+namespace aspire {
+namespace {
+
+Scratch& scratch() {
+  static thread_local Scratch sc;
+  return sc;
+}
+
+// Segments: per_head ? (row b, kv head g) at index b * num_kv_heads + g : row b, each with
+// its list start (kv_indices offset), list pages and kv length.
+int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const int32_t* seg_start,
+              const int32_t* seg_pages, const int32_t* seg_kv_len, int32_t batch, bool per_head,
+              int32_t num_qo_heads, int32_t num_kv_heads, int32_t causal, void* host_buf, aspire_plan_info* info) {
+  const int group = num_qo_heads / num_kv_heads;
   const aspire_plan_layout& L = *layout;
   const PlanOffsets off = plan_offsets(L);
-  ASPIRE_CHECK_ARG(host_buf_bytes >= off.total * 4, "host plan buffer smaller than the layout");
-  const int group = num_qo_heads / num_kv_heads;
   const int W = L.num_waves;
 
-  static thread_local Scratch sc;
+  Scratch& sc = scratch();
   for (auto& s : sc.segs) s.clear();
   sc.items.clear();
   sc.merges.clear();
 
-  // Row-shared page lists are planned head-aligned: the stream-K unit is a
-  // whole page (all kv heads) and a slot is a group of num_kv_heads
-  // consecutive waves, wave g of the group streaming kv head g. Every head of
-  // a page is then read at about the same time by waves dispatched together,
-  // which keeps the page's 64 KB of DRAM traffic together. Per-head lists are
-  // planned per (row, kv head) segment with single-wave slots.
-  const bool aligned = !per_head_lists && W % num_kv_heads == 0;
+  // Head-aligned planning: the stream-K unit is a whole page (all kv heads)
+  // and a slot is a group of num_kv_heads consecutive waves, wave g of the
+  // group streaming kv head g. Every head of a page is then read at about the
+  // same time by waves dispatched together, which keeps a shared page's 64 KB
+  // of DRAM traffic together. It needs every row's heads to attend the same
+  // number of tokens; otherwise each (row, kv head) is a segment of its own
+  // with single-wave slots.
+  bool uniform = true;
+  if (per_head)
+    for (int b = 0; b < batch && uniform; ++b)
+      for (int g = 1; g < num_kv_heads; ++g)
+        if (seg_kv_len[b * num_kv_heads + g] != seg_kv_len[b * num_kv_heads]) {
+          uniform = false;
+          break;
+        }
+  const bool aligned = uniform && W % num_kv_heads == 0;
   const int hpu = aligned ? num_kv_heads : 1;
   int max_rows = 0;
   int num_segments = 0;
@@ -146,22 +158,28 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
       max_rows = std::max(max_rows, rows);
       const int cls = (rows - 1) / 16;
       for (int g = 0; g < num_kv_heads; g += hpu) {
-        const int s = per_head_lists ? b * num_kv_heads + g : b;
-        const int kvl_row = kv_len[s];
-        const int list_pages = kv_indptr[s + 1] - kv_indptr[s];
-        if (kvl_row < 0 || list_pages < 0) {
+        const int s = per_head ? b * num_kv_heads + g : b;
+        const int kvl_row = seg_kv_len[s];
+        if (kvl_row < 0) {
           set_error("aspire_plan_build: segment %d has negative length", s);
           return ASPIRE_ERR_INVALID;
         }
         const int kvl = causal && tq < q_len ? std::max(kvl_row - q_len + t0 + tq, 0) : kvl_row;
         const int np = (kvl + kPage - 1) / kPage;
-        if (np > list_pages) {
-          set_error("aspire_plan_build: segment %d needs %d pages but its list holds %d", s, np,
-                    list_pages);
-          return ASPIRE_ERR_INVALID;
+        // every head the segment covers must hold the pages in its list
+        bool shared = true;
+        for (int gg = 0; gg < (per_head ? hpu : 1); ++gg) {
+          const int sg = s + gg;
+          if (seg_pages[sg] < 0 || np > seg_pages[sg]) {
+            set_error("aspire_plan_build: segment %d needs %d pages but its list holds %d", sg, np,
+                      seg_pages[sg]);
+            return ASPIRE_ERR_INVALID;
+          }
+          if (seg_start[sg] != seg_start[s]) shared = false;
         }
-        sc.segs[cls].push_back(
-            Segment{qo_indptr[b] + t0, tq, kvl, kv_indptr[s], np, (b << 8) | g, rows});
+        const int32_t direct = (hpu > 1 && !shared) ? kItemDirect : 0;
+        sc.segs[cls].push_back(Segment{qo_indptr[b] + t0, tq, kvl, seg_start[s], np, (b << 8) | g, rows,
+                                       per_head ? s : -1, direct});
         num_segments += hpu;
       }
     }
@@ -196,7 +214,8 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
         if (s.npages == 0) {
           const int64_t slot = (zero_rr++ % s_eff + rot) % slots;
           for (int gg = 0; gg < hpu; ++gg) {
-            WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, 0, 0, s.bg + gg, -1};
+            const int32_t base = s.seg0 >= 0 ? seg_start[s.seg0 + gg] : s.list_base;
+            WorkItem it{s.q_start, s.q_len | s.direct, s.kv_len, base, 0, 0, s.bg + gg, -1};
             sc.items.emplace_back(static_cast<int32_t>(slot * hpu + gg), it);
           }
           continue;
@@ -219,7 +238,8 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
           const int64_t k = j - j_lo;
           for (int gg = 0; gg < hpu; ++gg) {
             const int64_t prow = pieces > 1 ? first + (int64_t(gg) * pieces + k) * s.rows : -1;
-            WorkItem it{s.q_start, s.q_len, s.kv_len, s.list_base, static_cast<int32_t>(wb - a),
+            const int32_t base = s.seg0 >= 0 ? seg_start[s.seg0 + gg] : s.list_base;
+            WorkItem it{s.q_start, s.q_len | s.direct, s.kv_len, base, static_cast<int32_t>(wb - a),
                         static_cast<int32_t>(we - a), s.bg + gg, static_cast<int32_t>(prow)};
             sc.items.emplace_back(static_cast<int32_t>(((j + rot) % slots) * hpu + gg), it);
           }
@@ -282,6 +302,67 @@ extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t
                       int64_t(sc.merges.size()) * 8) *
                      4;
   return ASPIRE_OK;
+}
+
+int check_common(const aspire_plan_layout* layout, const int32_t* qo_indptr, int32_t batch, int32_t num_qo_heads,
+                 int32_t num_kv_heads, int32_t page_size, const void* host_buf, int64_t host_buf_bytes,
+                 const aspire_plan_info* info, const char* fn) {
+  if (!layout || !host_buf || !info) {
+    set_error("%s: null argument", fn);
+    return ASPIRE_ERR_INVALID;
+  }
+  const char* msg = nullptr;
+  if (batch < 0) msg = "negative batch";
+  else if (batch >= (1 << 23)) msg = "batch too large";
+  else if (batch > 0 && !qo_indptr) msg = "null plan array";
+  else if (page_size != kPage) msg = "page_size must be 16";
+  else if (num_kv_heads <= 0 || num_kv_heads >= 256) msg = "num_kv_heads must be in [1, 255]";
+  else if (num_qo_heads <= 0 || num_qo_heads % num_kv_heads != 0) msg = "num_qo_heads must be a multiple of num_kv_heads";
+  else if (host_buf_bytes < plan_offsets(*layout).total * 4) msg = "host plan buffer smaller than the layout";
+  if (msg) {
+    set_error("%s: %s", fn, msg);
+    return ASPIRE_ERR_INVALID;
+  }
+  return ASPIRE_OK;
+}
+
+}  // namespace
+}  // namespace aspire
+
+extern "C" int aspire_plan_build(const aspire_plan_layout* layout, const int32_t* qo_indptr,
+                                 const int32_t* kv_indptr, const int32_t* kv_len, int32_t batch,
+                                 int32_t per_head_lists, int32_t num_qo_heads,
+                                 int32_t num_kv_heads, int32_t page_size, int32_t causal,
+                                 void* host_buf, int64_t host_buf_bytes, aspire_plan_info* info) {
+  using namespace aspire;
+  int rc = check_common(layout, qo_indptr, batch, num_qo_heads, num_kv_heads, page_size, host_buf, host_buf_bytes,
+                        info, "aspire_plan_build");
+  if (rc != ASPIRE_OK) return rc;
+  ASPIRE_CHECK_ARG(batch == 0 || (kv_indptr && kv_len), "null plan array");
+  const int64_t n = per_head_lists ? int64_t(batch) * num_kv_heads : batch;
+  Scratch& sc = scratch();
+  sc.start.resize(std::max<int64_t>(n, 1));
+  sc.pages.resize(std::max<int64_t>(n, 1));
+  for (int64_t s = 0; s < n; ++s) {
+    sc.start[s] = kv_indptr[s];
+    sc.pages[s] = kv_indptr[s + 1] - kv_indptr[s];
+  }
+  return plan_core(layout, qo_indptr, sc.start.data(), sc.pages.data(), kv_len, batch, per_head_lists != 0,
+                   num_qo_heads, num_kv_heads, causal, host_buf, info);
+}
+
+extern "C" int aspire_plan_build_segments(const aspire_plan_layout* layout, const int32_t* qo_indptr,
+                                          const int32_t* seg_start, const int32_t* seg_pages,
+                                          const int32_t* seg_kv_len, int32_t batch, int32_t num_qo_heads,
+                                          int32_t num_kv_heads, int32_t page_size, int32_t causal,
+                                          void* host_buf, int64_t host_buf_bytes, aspire_plan_info* info) {
+  using namespace aspire;
+  int rc = check_common(layout, qo_indptr, batch, num_qo_heads, num_kv_heads, page_size, host_buf, host_buf_bytes,
+                        info, "aspire_plan_build_segments");
+  if (rc != ASPIRE_OK) return rc;
+  ASPIRE_CHECK_ARG(batch == 0 || (seg_start && seg_pages && seg_kv_len), "null plan array");
+  return plan_core(layout, qo_indptr, seg_start, seg_pages, seg_kv_len, batch, true, num_qo_heads, num_kv_heads,
+                   causal, host_buf, info);
 }
 
 extern "C" int aspire_plan_upload(const aspire_plan_layout* layout, const aspire_plan_info* info,

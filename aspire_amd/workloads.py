@@ -201,3 +201,34 @@ def config4(device="cpu", seed=0, draft_frac: float = 0.0, batch: int = 16, lo: 
     q_len = np.where(is_draft, 1, rng.integers(2, 10, size=batch))
     return build_step(hq=32, hkv=8, ctx_len=ctx, q_len=q_len, is_draft=is_draft, draft_budget=draft_budget,
                       seed=seed, device=device)
+
+
+def config3_rows(seed=0, batch: int = 64, lo: int = 8192, hi: int = 32768, draft_frac: float = 0.5,
+                 q_lo: int = 2, q_hi: int = 9):
+    """Rows of the full decode step: contexts U[lo, hi] (tokens after the append);
+    round(draft_frac * batch) rows, chosen by a seeded permutation, draft (q_len 1)
+    and the others verify with q_len U{q_lo..q_hi}. Returns (ctx_len, q_len, is_draft)."""
+    rng = np.random.default_rng(seed + 3000)
+    ctx = rng.integers(lo, hi + 1, size=batch).astype(np.int64)
+    is_draft = np.zeros(batch, dtype=bool)
+    is_draft[rng.permutation(batch)[: int(round(draft_frac * batch))]] = True
+    q_len = np.where(is_draft, 1, rng.integers(q_lo, q_hi + 1, size=batch)).astype(np.int64)
+    return ctx, q_len, is_draft
+
+
+def random_block_table(pages_per_row, seed=0, pool_pages: int | None = None) -> tuple[np.ndarray, int]:
+    """[B, max pages] int32 logical -> physical table drawn from a seeded
+    permutation of the pool (default: exactly the pages the rows need)."""
+    pages_per_row = np.asarray(pages_per_row, dtype=np.int64)
+    total = int(pages_per_row.sum())
+    pool = total if pool_pages is None else int(pool_pages)
+    if pool < total:
+        raise ValueError("pool smaller than the pages the rows need")
+    perm = np.random.default_rng(seed + 77).permutation(pool).astype(np.int32)
+    width = int(pages_per_row.max()) if pages_per_row.size else 0
+    table = np.zeros((pages_per_row.size, width), dtype=np.int32)
+    off = 0
+    for b, n in enumerate(pages_per_row):
+        table[b, :n] = perm[off : off + n]
+        off += int(n)
+    return table, pool

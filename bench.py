@@ -63,12 +63,16 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=1, choices=[1, 2])
+    ap.add_argument("--config", type=int, default=1, choices=[1, 2, 3],
+                    help="1: mixed layer (default, also runs the components, config 4 and the config-3 decode "
+                         "step); 2: refresh layer; 3: the full 36-layer decode step alone")
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-components", action="store_true",
                     help="skip the per-component measurements (append, page list, merge, selectors, refresh layer)")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-3 full decode step")
+    ap.add_argument("--decode-steps", type=int, default=30, help="timed graph replays of the config-3 step")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (read + write) for rocprofv3 counter calibration")
     return ap.parse_args()
@@ -169,6 +173,18 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(_lib.build_info())
+    if args.config == 3:
+        dec = measure_config3(args.decode_steps, min(args.warmup, 20), args.waves_per_cu)
+        line = {
+            "metric": "decode tokens/s (Qwen3-8B shape, 36 layers, B=64, ctx U[8k,32k], 50/50 draft/verify)",
+            "value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.decode_steps,
+            "warmup": min(args.warmup, 20), "ms_per_step": dec["step_ms"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (random-init bf16 weights, N(0,1) KV pages, random-permutation page pool)",
+            "config": {"workload": dec["workload"], **{k: v for k, v in dec.items() if k != "workload"}},
+        }
+        print(json.dumps(line), flush=True)
+        return
     t0 = time.time()
     step = config1(device=dev) if args.config == 1 else config2(device=dev)
     torch.cuda.synchronize()
@@ -240,6 +256,9 @@ def main():
     if args.config == 1 and not args.no_components:
         components = measure_components(step, w, out, min(args.steps, 50), plan_us)
         components["long_context_config4"] = measure_config4(min(args.steps, 100), args.waves_per_cu)
+    decode = None
+    if args.config == 1 and not args.no_decode:
+        decode = measure_config3(args.decode_steps, min(args.warmup, 20), args.waves_per_cu)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -291,6 +310,7 @@ def main():
             "bytes_per_launch": attn_bytes,
         },
         "cpu_baseline": cpu,
+        "decode": decode,
         "components": components,
     }
     print(json.dumps(line), flush=True)
@@ -551,6 +571,88 @@ def measure_config4(steps, waves_per_cu, fracs=(0.0, 0.25, 0.5, 0.75, 1.0)):
             f"items {list(info.num_items)}, merges {info.num_merge}; per class {per_class}")
         del st, w, out
         torch.cuda.empty_cache()
+    return res
+
+
+def measure_config3(steps, warmup, waves_per_cu):
+    """Config 3: one full 36-layer Qwen3-8B decode step (batch 64, contexts U[8k, 32k], 32 draft rows
+    over top-128 per-KV-head page lists refreshed at layer 2, 32 verify rows with q_len U{2..9}),
+    recorded in one HIP graph and replayed. Returns tokens/s, step time and the attention share."""
+    from aspire_amd.decode_step import QWEN3_8B, DecodeWeights, MixedDecodeStep, alloc_kv_caches
+    from aspire_amd.workloads import PAGE, config3_rows, random_block_table
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    shape = QWEN3_8B
+    ctx, ql, dr = config3_rows(seed=0)
+    n_pages = (ctx + PAGE - 1) // PAGE
+    table, pool = random_block_table(n_pages, seed=0)
+    t0 = time.time()
+    weights = DecodeWeights(shape, dev, seed=0)
+    caches = alloc_kv_caches(shape, pool, dev, seed=0)
+    step = MixedDecodeStep(weights, caches, ctx, ql, dr, torch.from_numpy(table), budget=128, refresh_layer=2,
+                           waves_per_cu=waves_per_cu)
+    torch.cuda.synchronize()
+    log(f"config3: built in {time.time() - t0:.1f}s: {int(dr.sum())} draft + {int((~dr).sum())} verify rows, "
+        f"{step.T} tokens, pool {pool} pages x {shape.n_layer} layers "
+        f"({caches.numel() * 2 / 1e9:.1f} GB KV), weights {(shape.n_layer * weights.layer_bytes() + 2 * weights.output.numel() * 2) / 1e9:.1f} GB")
+    reps = 10
+    tp = time.perf_counter()
+    for _ in range(reps):
+        step.plan()
+    plan_us = (time.perf_counter() - tp) / reps * 1e6
+    torch.cuda.synchronize()
+    for _ in range(3):
+        step.forward()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    eager_n = 5
+    eager_ms = timed(step.forward, eager_n, stream)
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        step.forward()
+    stream.wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step.forward()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = timed(graph.replay, steps, stream)
+    attn_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(attn_graph):
+        step.attention_only()
+    for _ in range(3):
+        attn_graph.replay()
+    attn_ms = timed(attn_graph.replay, steps, stream)
+    nb = step.algorithmic_bytes()
+    tps = step.T / (ms * 1e-3)
+    gbs = nb["total"] / (ms * 1e-3) / 1e9
+    attn_gbs = nb["kv"] / (attn_ms * 1e-3) / 1e9
+    log(f"config3: step {ms:.2f} ms (eager {eager_ms:.2f} ms) -> {tps:.0f} tokens/s, {gbs:.0f} GB/s; "
+        f"attention {attn_ms:.2f} ms ({attn_ms / ms:.1%}) at {attn_gbs:.0f} GB/s; "
+        f"measured in {time.perf_counter() - t1:.1f}s")
+    res = {
+        "workload": ("config3: full 36-layer Qwen3-8B decode step (hidden 4096, 32/8 heads, SwiGLU 12288, "
+                     "qk-norm, RoPE 1e6), batch 64, contexts U[8192, 32768], 32 draft rows (q_len 1, top-128 "
+                     "pages per KV head by key-mean score, refreshed at layer 2) + 32 verify rows (q_len "
+                     "U{2..9}); one HIP graph per step, greedy token pick"),
+        "tokens_per_s": round(tps, 1),
+        "step_ms": round(ms, 3),
+        "eager_step_ms": round(eager_ms, 3),
+        "tokens_per_step": step.T,
+        "algorithmic_bytes": nb,
+        "step_gbs": round(gbs, 1),
+        "step_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+        "attention_ms": round(attn_ms, 3),
+        "attention_share": round(attn_ms / ms, 4),
+        "attention_kv_gbs": round(attn_gbs, 1),
+        "plan_host_us": round(plan_us, 1),
+        "verify_q_len": ql[~dr].tolist(),
+    }
+    del graph, attn_graph, step, caches, weights
+    torch.cuda.empty_cache()
     return res
 
 

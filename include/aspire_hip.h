@@ -97,6 +97,26 @@ int aspire_build_mixed_page_list(const void* mode_flags, int32_t mode_flags_elem
                                  int32_t* paged_kv_indptr, int32_t indptr_fill_to,
                                  void* stream);
 
+/* Per-(row, kv head) page lists: the consumer of the key-mean (B) selection,
+ * which has no reference code (the BASELINE config-2 refresh layer feeding the
+ * following sparse layers). Segment s = b * num_kv_heads + g takes
+ * selected_counts[s] entries of row s of `selected` ([batch * num_kv_heads,
+ * selected_width], the KeyMeanPageSelector output) when row b drafts, and
+ * verify_num_pages[b] entries of verify row b otherwise: once per head, or,
+ * with share_verify, once per row with all the row's heads starting at that
+ * list. paged_kv_indptr[s] receives segment s's first entry and
+ * paged_kv_indptr[batch * num_kv_heads] the total (without sharing this is the
+ * running count, the per-head form of aspire_build_mixed_page_list's indptr);
+ * entries up to indptr_fill_to repeat the total. Same bounds and error rules
+ * as aspire_build_mixed_page_list. */
+int aspire_build_head_page_lists(const void* mode_flags, int32_t mode_flags_elem_size,
+                                 const int32_t* selected, int64_t selected_width,
+                                 const int32_t* selected_counts, const int32_t* verify_indices,
+                                 int64_t verify_width, int64_t verify_rows,
+                                 const int32_t* verify_num_pages, int32_t batch, int32_t num_kv_heads,
+                                 int32_t share_verify, int32_t* paged_kv_indices, int64_t indices_capacity,
+                                 int32_t* paged_kv_indptr, int32_t indptr_fill_to, void* stream);
+
 /* ---------------------------------------------------------------- (a7) -- */
 /* Work plan for the mixed attention kernel. Replaces the patched FlashInfer
  * TwoStageHolisticPlan (third_party/flashinfer/aspire.patch:108-288) behind
@@ -146,6 +166,19 @@ int aspire_plan_build(const aspire_plan_layout* layout, const int32_t* qo_indptr
                       int32_t num_kv_heads, int32_t page_size, int32_t causal,
                       void* host_buf, int64_t host_buf_bytes,
                       aspire_plan_info* info);
+
+/* The plan of aspire_plan_build from explicit (row, kv head) segments, for
+ * page lists that are neither one per row nor laid end to end per head (no
+ * reference counterpart: the per-head lists of the key-mean selection, with
+ * verify rows sharing one list). Segment s = b * num_kv_heads + g streams
+ * seg_kv_len[s] tokens of the seg_pages[s] entries at kv_indices[seg_start[s]].
+ * When every row's heads have the same length the plan is head-aligned: rows
+ * whose heads share one start stage their pages through LDS like row lists,
+ * rows with a list per head load their own head's rows. */
+int aspire_plan_build_segments(const aspire_plan_layout* layout, const int32_t* qo_indptr,
+                               const int32_t* seg_start, const int32_t* seg_pages, const int32_t* seg_kv_len,
+                               int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t page_size,
+                               int32_t causal, void* host_buf, int64_t host_buf_bytes, aspire_plan_info* info);
 
 int aspire_plan_upload(const aspire_plan_layout* layout, const aspire_plan_info* info,
                        const void* host_buf, void* dev_buf, void* stream);
@@ -360,6 +393,31 @@ int aspire_qk_norm_rope_append(const aspire_rope_args* args, void* stream);
 int aspire_rope_frequencies(int32_t head_dim, float rope_theta, float rope_scale, int32_t llama31,
                             float low_freq_factor, float high_freq_factor, float old_context_len,
                             float* out);
+
+/* ------------------------------------------------ decode-step row operations
+ * The per-token steps a decode step runs between the GEMMs, used by the full
+ * decode step. One workgroup per row, no scratch memory.
+ *
+ * aspire_add_rms_norm: with delta, x[r] += delta[r] (bf16) first
+ * (h = x + attn_out, aspire/models/sparse_draft_transformer.py:232-238); then
+ * out[r] = RMSNorm(x[r]) * weight as transformer.py:505-516 computes it in
+ * bf16. dim % 8 == 0, dim <= 8192, 16-byte aligned rows; out must not overlap
+ * x or delta. */
+int aspire_add_rms_norm(void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                        const void* weight, void* out, int64_t out_stride, int32_t rows, int32_t dim,
+                        float eps, void* stream);
+
+/* SwiGLU's elementwise step, FeedForward.forward (transformer.py:498-499):
+ * out[t, i] = bf16(bf16(silu(gate_up[t, i])) * gate_up[t, inter + i]), the
+ * gate (w1) and up (w3) projections side by side in one row. */
+int aspire_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t out_stride,
+                    int32_t rows, int32_t inter, void* stream);
+
+/* Greedy token pick (the top_k == 0 branch of TransformerSparseDraft.unified_forward,
+ * sparse_draft_transformer.py:276-286): ids[r] = the first index of the
+ * maximum of the bf16 row logits[r, :vocab] (torch.argmax). */
+int aspire_argmax_rows(const void* logits, int64_t stride, int32_t rows, int32_t vocab, int64_t* ids,
+                       void* stream);
 
 #ifdef __cplusplus
 }

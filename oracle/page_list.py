@@ -57,3 +57,36 @@ def fill_padding_rows(paged_kv_indptr: np.ndarray, last_page_len: np.ndarray, bs
     """base.py:1253-1256: padding rows repeat the final indptr and have no last page."""
     paged_kv_indptr[bsz + 1 :] = paged_kv_indptr[bsz]
     last_page_len[bsz:] = 0
+
+
+def build_head_page_lists(mode_flags, selected, selected_counts, verify_indices, verify_num_pages,
+                          paged_kv_indices: np.ndarray, paged_kv_indptr: np.ndarray,
+                          share_verify: bool = False) -> None:
+    """Per-(row, kv head) segments (no reference code: the consumer of the key-mean
+    selection). Segment ``b*H + g`` is ``selected[b, g, :counts[b, g]]`` for a draft row
+    and ``verify_indices[b, :verify_num_pages[b]]`` otherwise, written once per head or,
+    with ``share_verify``, once per row. ``paged_kv_indptr[s]`` is segment ``s``'s first
+    entry and ``paged_kv_indptr[B*H]`` the total. With one head and no sharing this is
+    ``build_unified_indices`` above."""
+    mode_flags = np.asarray(mode_flags)
+    selected = np.asarray(selected)
+    counts = np.asarray(selected_counts)
+    bsz, heads = mode_flags.shape[0], selected.shape[1]
+    pos = 0
+    for b in range(bsz):
+        row_start = pos
+        for g in range(heads):
+            if mode_flags[b] == DRAFT_MODE:
+                paged_kv_indptr[b * heads + g] = pos
+                src = selected[b, g, : int(counts[b, g])]
+            elif share_verify:
+                paged_kv_indptr[b * heads + g] = row_start
+                if g > 0:
+                    continue
+                src = np.asarray(verify_indices)[b, : int(verify_num_pages[b])]
+            else:
+                paged_kv_indptr[b * heads + g] = pos
+                src = np.asarray(verify_indices)[b, : int(verify_num_pages[b])]
+            paged_kv_indices[pos : pos + len(src)] = src
+            pos += len(src)
+    paged_kv_indptr[bsz * heads] = pos

@@ -170,6 +170,58 @@ def test_per_head_page_lists(gpu):
     assert (lse.cpu() - ref_lse).abs().max() < 2e-3
 
 
+@pytest.mark.parametrize("wpc", [None, 8])
+def test_segment_plan_shared_and_per_head_rows(gpu, wpc):
+    """plan_segments: verify rows share one list across heads (staged path), draft rows
+    read one list per head (direct path) in the same head-aligned launch."""
+    say("segment plan", wpc)
+    hq, hkv = 32, 8
+    ctx = np.array([3000, 1000, 2500, 700, 4000, 333, 1600])
+    ql = np.array([1, 4, 1, 9, 1, 7, 2])
+    draft = ql == 1
+    step = build_step(hq=hq, hkv=hkv, ctx_len=ctx, q_len=ql, is_draft=[0] * len(ctx), draft_budget=0, seed=21,
+                      device=gpu)
+    table = step.block_table.cpu().numpy()
+    rng = np.random.default_rng(7)
+    n_pages = (ctx + 15) // 16
+    last = (ctx - 1) % 16 + 1
+    idx, start, pages, kvl = [], [], [], []
+    pos = 0
+    for b in range(len(ctx)):
+        n = int(n_pages[b])
+        if draft[b]:
+            k = min(24, n)
+            for g in range(hkv):
+                sel = np.sort(np.concatenate([rng.choice(n - 1, size=k - 1, replace=False), [n - 1]]))
+                idx.append(table[b, sel])
+                start.append(pos)
+                pos += k
+                pages.append(k)
+                kvl.append((k - 1) * 16 + last[b])
+        else:
+            idx.append(table[b, :n])
+            start += [pos] * hkv
+            pages += [n] * hkv
+            kvl += [int(ctx[b])] * hkv
+            pos += n
+    flat = np.concatenate(idx).astype(np.int32)
+    w = make_wrapper(gpu, waves_per_cu=wpc)
+    plan(w, step)
+    t32 = lambda a: torch.tensor(np.asarray(a), dtype=torch.int32)
+    w.plan_segments(step.qo_indptr_host[: len(ctx) + 1], t32(start), t32(pages), t32(kvl),
+                    torch.from_numpy(flat).to(gpu), hq, hkv, 128, PAGE, causal=True)
+    out, lse = w.run(step.q, step.cache, return_lse=True)
+    torch.cuda.synchronize()
+    # the oracle takes per-head lists laid end to end
+    kvp_o = np.concatenate([[0], np.cumsum(pages)])
+    idx_o = np.concatenate([flat[s0 : s0 + n] for s0, n in zip(start, pages)])
+    ref_out, ref_lse = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host[: len(ctx) + 1], kvp_o,
+                                       torch.from_numpy(idx_o), kvl, num_kv_heads=hkv, per_head_lists=True)
+    T = int(ql.sum())
+    attn_close(out[:T], ref_out[:T])
+    assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
+
+
 @pytest.mark.parametrize("kind", ["first_last_compact", "last_token"])
 def test_logits_dump(gpu, kind):
     say("dump", kind)

@@ -74,9 +74,14 @@ def expected_tiles(q_len, kv_len, group, causal=True):
             for t0 in range(0, q_len, tile)]
 
 
-def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False, causal=True):
+DIRECT = 1 << 16  # item flag: heads of a head-aligned row read different lists
+
+
+def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False, causal=True, seg_start=None):
     classes, merges = decode(lay, buf, info)
     group = hq // hkv
+    hpu = int(buf[4])
+    starts = np.asarray(seg_start) if seg_start is not None else np.asarray(kvp)[: len(kvl)]
     seen = {}
     partial_rows = set()
     for c, (ip, it) in enumerate(classes):
@@ -84,14 +89,17 @@ def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False, causal=Tr
         for w in range(lay.num_waves):
             for row in it[ip[w] : ip[w + 1]]:
                 q_start, q_len, kv_len, base, pb, pe, bg, prow = row.tolist()
+                flag, q_len = q_len & DIRECT, q_len & (DIRECT - 1)
                 b, g = bg >> 8, bg & 255
+                shared = not per_head or len(set(starts[b * hkv : (b + 1) * hkv].tolist())) == 1
+                assert bool(flag) == (hpu > 1 and not shared), (b, g, flag, hpu)
                 assert (q_len * group - 1) // 16 == c
                 seg = b * hkv + g if per_head else b
                 tiles = {t0: (tq, keys) for t0, tq, keys in
                          expected_tiles(qo[b + 1] - qo[b], kvl[seg], group, causal)}
                 t0 = q_start - qo[b]
                 assert t0 in tiles and (q_len, kv_len) == tiles[t0], (b, t0, q_len, kv_len)
-                assert base == kvp[seg] and pe <= (kv_len + 15) // 16
+                assert base == starts[seg] and pe <= (kv_len + 15) // 16
                 for p in range(pb, pe):
                     key = (b, g, t0, p)
                     assert key not in seen, f"page {key} planned twice"
@@ -162,7 +170,14 @@ def test_per_head_lists():
     qo = np.array([0, 1, 2, 3])
     lay = layout(num_cus=8, waves_per_cu=4)
     buf, info = plan(lay, qo, kvp, kvl, hq, hkv, per_head=True)
+    assert int(buf[4]) == 1  # heads of a row differ in length: one wave per (row, head)
     check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=True)
+    # one length per row: head-aligned slots, every row's heads on their own lists (flagged)
+    kvl_u = np.repeat(kvl[::hkv], hkv)
+    kvp_u = np.concatenate([[0], np.cumsum((kvl_u + 15) // 16)])
+    buf, info = plan(lay, qo, kvp_u, kvl_u, hq, hkv, per_head=True)
+    assert int(buf[4]) == hkv
+    check_cover(lay, buf, info, qo, kvp_u, kvl_u, hq, hkv, per_head=True)
 
 
 def test_rejects_bad_inputs():
@@ -201,3 +216,55 @@ def test_prefill_rows_split_into_query_tiles(causal):
     # the first tile of the second row only needs the keys up to its 12th token
     if causal:
         assert expected_tiles(1000, 1000, 4)[0] == (0, 12, 12)
+
+
+def plan_segments(lay, qo, start, pages, kvl, hq, hkv, causal=True):
+    buf = np.zeros(8 << 18, dtype=np.int32)
+    info = _lib.PlanInfo()
+    arr = lambda a: np.ascontiguousarray(a, dtype=np.int32)
+    qo, start, pages, kvl = arr(qo), arr(start), arr(pages), arr(kvl)
+    rc = _lib.lib().aspire_plan_build_segments(
+        ctypes.byref(lay), qo.ctypes.data_as(ctypes.c_void_p), start.ctypes.data_as(ctypes.c_void_p),
+        pages.ctypes.data_as(ctypes.c_void_p), kvl.ctypes.data_as(ctypes.c_void_p), len(kvl) // hkv, hq, hkv, 16,
+        int(causal), buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, ctypes.byref(info))
+    _lib.check(rc, "plan_segments")
+    return buf, info
+
+
+def test_segments_shared_and_per_head_rows():
+    """Verify rows share one list across heads (staged), draft rows hold one per head (flagged
+    direct); all heads of a row have one length, so the plan is head-aligned."""
+    hq, hkv = 32, 8
+    rng = np.random.default_rng(2)
+    ctx = np.array([5000, 700, 3000, 123, 64, 2000])
+    ql = np.array([1, 4, 1, 9, 1, 2])
+    draft = ql == 1
+    cnt = np.where(draft, np.minimum(40, (ctx + 15) // 16), (ctx + 15) // 16)
+    start = np.zeros((len(ctx), hkv), dtype=np.int64)
+    pos = 0
+    for b in range(len(ctx)):
+        if draft[b]:
+            start[b] = pos + cnt[b] * np.arange(hkv)
+            pos += cnt[b] * hkv
+        else:
+            start[b] = pos
+            pos += cnt[b]
+    start = start.reshape(-1)
+    pages = np.repeat(cnt, hkv)
+    kvl = np.repeat((cnt - 1) * 16 + (ctx - 1) % 16 + 1, hkv)
+    qo = np.concatenate([[0], np.cumsum(ql)])
+    lay = layout(num_cus=16, waves_per_cu=4)
+    buf, info = plan_segments(lay, qo, start, pages, kvl, hq, hkv)
+    assert int(buf[4]) == hkv
+    check_cover(lay, buf, info, qo, None, kvl, hq, hkv, per_head=True, seg_start=start)
+    # one head of one row longer than its siblings: per-(row, head) slots, no flags
+    kvl2 = kvl.copy()
+    kvl2[3] -= 16
+    buf2, info2 = plan_segments(lay, qo, start, pages, kvl2, hq, hkv)
+    assert int(buf2[4]) == 1
+    check_cover(lay, buf2, info2, qo, None, kvl2, hq, hkv, per_head=True, seg_start=start)
+    # a list shorter than its length is rejected
+    with pytest.raises(ValueError, match="pages"):
+        bad = pages.copy()
+        bad[5] -= 1
+        plan_segments(lay, qo, start, bad, kvl, hq, hkv)
