@@ -21,6 +21,8 @@
 //     reduced across the 4 lane groups with permlane swaps (no LDS).
 // A row tile is 16 query rows; NT tiles share the K/V registers
 // (q_len * group <= 16 * NT). One persistent launch runs every class.
+#include <type_traits>
+
 #include "common.h"
 
 namespace aspire {
@@ -232,7 +234,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 
   // Per-page compute. after_qk runs once QK^T has consumed K, after_pv once
   // P.V has consumed V (the half-page pipeline issues the next loads there).
-  auto page_body = [&](int pg, const uint4 (&kr)[4], const uint4 (&vr)[4], auto&& after_qk, auto&& after_pv) {
+  // vsrc: the page's V rows as loaded (uint4[4], lane r = key r, transposed
+  // here) or its V^T fragments ready for the PV MFMA (i16x4[8], one per
+  // 16-dim slice j, read transposed from LDS).
+  auto page_body = [&](int pg, const uint4 (&kr)[4], const auto& vsrc, auto&& after_qk, auto&& after_pv) {
       const int base_pos = pg * 16 + grp * 4;
 
       f32x4 s[NT];
@@ -321,14 +326,20 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
           for (int j = 0; j < 8; ++j) acc[t][j] *= alpha[t];
       }
 
-      // O^T += V^T P^T, one 16-dim slice at a time: transpose the slice with an
-      // exact identity MFMA (the values are bf16 already), then accumulate.
+      // O^T += V^T P^T, one 16-dim slice at a time. Rows from registers are
+      // transposed with an exact identity MFMA (the values are bf16 already).
+      constexpr bool kVt = std::is_same_v<std::remove_cv_t<std::remove_reference_t<decltype(vsrc)>>, i16x4[8]>;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const uint4 src = vr[j >> 1];
-        const i16x4 va = (j & 1) ? as_i16x4(src.z, src.w) : as_i16x4(src.x, src.y);
-        const f32x4 d = mfma_16x16x16_bf16(va, ident, f32x4{0.f, 0.f, 0.f, 0.f});
-        const i16x4 vt = as_i16x4(pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3]));
+        i16x4 vt;
+        if constexpr (kVt) {
+          vt = vsrc[j];
+        } else {
+          const uint4 src = vsrc[j >> 1];
+          const i16x4 va = (j & 1) ? as_i16x4(src.z, src.w) : as_i16x4(src.x, src.y);
+          const f32x4 d = mfma_16x16x16_bf16(va, ident, f32x4{0.f, 0.f, 0.f, 0.f});
+          vt = as_i16x4(pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3]));
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t][j] = mfma_16x16x16_bf16(vt, pf[t], acc[t][j]);
       }
@@ -376,6 +387,23 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 #pragma unroll
           for (int c = 0; c < 4; ++c) dst[c] = base[(gl * 16 + c * 4 + grp) ^ r];
         };
+        // V^T fragments straight from the staged rows with the LDS transpose
+        // read: of the 16 lanes of group grp, lane r addresses key row
+        // 4*grp + r/4 at dims 32*(j/2) + 8*(r%4) + 4*(j%2) (4 consecutive
+        // bf16), and the read hands lane r element r%4 of the lanes r/4 + 4e,
+        // e = 0..3: keys 4*grp + e of dim 32*(j/2) + 8*(r/4) + 4*(j%2) + r%4,
+        // the A operand of the PV MFMA in the slice order of the epilogue.
+        const int vt_row = 4 * grp + (r >> 2);
+        auto read_vt = [&](int buf, i16x4(&vt)[8]) {
+          const char* base = reinterpret_cast<const char*>(stage_lds + buf * kStageBuf + kStageKv +
+                                                           vt_row * kStageRowChunks);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int chunk = (gl * 16 + 4 * (j >> 1) + (r & 3)) ^ vt_row;
+            vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(base + chunk * 16 + 8 * (j & 1)));
+          }
+        };
         uint4 st[8];
         stage_load(page_id(pb), true, st);
         stage_store(0, st);
@@ -385,15 +413,38 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
         int pg = pb;
         do {
           const int buf = (pg - pb) & 1;
-          uint4 kr[4], vr[4];
+          uint4 kr[4];
+          // V^T by transpose reads for 2-tile items; 1-tile items read V rows
+          // (conflict-free 128-bit reads) and transpose them with the identity
+          // MFMA, which measured faster there
+          using VSrc = std::conditional_t<(NT >= 2), i16x4[8], uint4[4]>;
+          VSrc vs;
           read_rows(buf, 0, kr);
-          const bool v_ok = pg * 16 + r < kv_len;  // rows past kv_len may hold stale values
           page_body(
-              pg, kr, vr,
+              pg, kr, vs,
               [&] {
-                read_rows(buf, 1, vr);
+                // keys past kv_len (only on a segment's last page) may hold stale
+                // values: zero them so 0 * stale cannot reach the sums
+                const bool tail = pg * 16 + 16 > kv_len;
+                if constexpr (NT >= 2) {
+                  read_vt(buf, vs);
+                  if (tail) {
+                    const int k0 = pg * 16 + 4 * grp;
+                    const uint32_t m0 = (k0 < kv_len ? 0xffffu : 0u) | (k0 + 1 < kv_len ? 0xffff0000u : 0u);
+                    const uint32_t m1 = (k0 + 2 < kv_len ? 0xffffu : 0u) | (k0 + 3 < kv_len ? 0xffff0000u : 0u);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) vr[c] = v_ok ? vr[c] : make_uint4(0, 0, 0, 0);
+                    for (int j = 0; j < 8; ++j) {
+                      const uint2 w = __builtin_bit_cast(uint2, vs[j]);
+                      vs[j] = as_i16x4(w.x & m0, w.y & m1);
+                    }
+                  }
+                } else {
+                  read_rows(buf, 1, vs);
+                  // a per-lane select here measured faster than the tail-only mask
+                  const bool v_ok = pg * 16 + r < kv_len;
+#pragma unroll
+                  for (int c = 0; c < 4; ++c) vs[c] = v_ok ? vs[c] : make_uint4(0, 0, 0, 0);
+                }
               },
               [&] {
                 stage_store(buf ^ 1, st);
