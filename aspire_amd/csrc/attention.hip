@@ -204,6 +204,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     for (int j = 0; j < 8; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // smallest causal limit of the item's rows (its first query token)
+  const int min_limit = p.causal ? min(kv_len - it.q_len, kv_len - 1) : kv_len - 1;
   const bool do_dump = p.dump_kind != 0 && (p.dump_flags == nullptr || p.dump_flags[b] != 0);
   const bool do_score = p.page_scores != nullptr && it.q_len == 1;
   float score_buf = 0.f;
@@ -295,8 +297,13 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 
         float x[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          x[i] = (base_pos + i <= limit[t]) ? s[t][i] * p.scale_log2 : kNegInf;
+        for (int i = 0; i < 4; ++i) x[i] = s[t][i] * p.scale_log2;
+        // only pages that reach a row's causal limit or kv_len need the mask
+        // (rows past the tile keep their unmasked, finite, unused values)
+        if (pg * 16 + 15 > min_limit) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = (base_pos + i <= limit[t]) ? x[i] : kNegInf;
+        }
         float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
         mx = max_xor32(max_xor16(mx));
         const float m_new = fmaxf(m[t], mx);

@@ -135,8 +135,12 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
+// Two fp32 values rounded to nearest-even bf16 in one instruction
+// (v_cvt_pk_bf16_f32); equal to bf16_rne_bits on every finite input.
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
-  return bf16_rne_bits(lo) | (bf16_rne_bits(hi) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 // fp32 values that are exactly representable in bf16: keep the upper halves.
 __device__ __forceinline__ uint32_t pack_bf16x2_exact(float lo, float hi) {
