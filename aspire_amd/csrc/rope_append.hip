@@ -2,10 +2,10 @@
 //
 // Per layer the reference runs q_norm, k_norm, two permutes, mylib::rope and
 // mylib::update_kv_padded (aspire/models/sparse_draft_transformer.py:149-171):
-// six launches and four round trips of q / k through HBM. Here one workgroup
-// handles one token: each wave takes whole heads (lane i owns rotated pair i,
-// i.e. dims 2i and 2i+1 after the permute), normalises, rotates and writes q
-// in place and k / v into the page pool at the token's append position.
+// six launches and four round trips of q / k through HBM. Here one wave
+// handles one head of one token (lane i owns rotated pair i, i.e. dims 2i and
+// 2i+1 after the permute): it normalises, rotates and writes q in place and
+// k / v into the page pool at the token's append position.
 //
 //   * RMSNorm (transformer.py:505-516): fp32 sum of squares (wave sum),
 //     x * (1 / sqrt(mean + eps)) rounded to bf16, times the bf16 weight,
@@ -17,6 +17,7 @@
 //     frequencies once, including the Llama 3.1 smoothing), accurate sincosf,
 //     (a, b) -> (a cos - b sin, b cos + a sin) in fp32, rounded to bf16;
 //   * append: the row / slot rule of the plain append (append_locate).
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -55,10 +56,16 @@ struct RopeParams {
 __device__ __forceinline__ float bf16_to_f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
 __device__ __forceinline__ uint16_t f_to_bf16(float f) { return static_cast<uint16_t>(bf16_rne_bits(f)); }
 
+constexpr int kHeadsPerBlock = 4;  // one wave per head
+
+// Grid (tokens, ceil((hq + hkv) / 4)): wave w of block (tok, hb) prepares
+// head 4 * hb + w of token tok (q heads first, then k heads) and, when
+// 4 * hb + w < hkv, copies that v head into the page.
 __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(RopeParams p) {
   const int tok = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int h = blockIdx.y * kHeadsPerBlock + wave;
   // rope position: row b of indptr owns tok (last b with indptr[b] <= tok < indptr[b + 1])
   int pos = -1;
   {
@@ -81,12 +88,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(RopeParams p) 
   uint16_t* page_k = nullptr;
   if (append) page_k = p.cache + int64_t(p.page_indices[entry]) * p.c_sp + int64_t(slot) * p.c_st;
 
-  float c = 1.f, s = 0.f;
-  if (pos >= 0) sincosf(static_cast<float>(pos) * p.freq[lane], &s, &c);
-  const int in0 = p.permute ? lane : 2 * lane;
-  const int in1 = p.permute ? lane + kPairs : 2 * lane + 1;
-
-  for (int h = wave; h < p.hq + p.hkv; h += 4) {
+  if (h < p.hq + p.hkv) {
+    float c = 1.f, s = 0.f;
+    if (pos >= 0) sincosf(static_cast<float>(pos) * p.freq[lane], &s, &c);
+    const int in0 = p.permute ? lane : 2 * lane;
+    const int in1 = p.permute ? lane + kPairs : 2 * lane + 1;
     const bool is_q = h < p.hq;
     uint16_t* row = is_q ? p.q + int64_t(tok) * p.q_st + int64_t(h) * p.q_sh
                          : p.k + int64_t(tok) * p.k_st + int64_t(h - p.hq) * p.k_sh;
@@ -110,14 +116,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(RopeParams p) 
     if (!is_q && append)
       *reinterpret_cast<uint32_t*>(page_k + int64_t(h - p.hq) * p.c_sh + 2 * lane) = packed;
   }
-  if (append && p.v != nullptr) {
+  if (append && p.v != nullptr && h < p.hkv && lane < kHeadDim / 8) {
     uint16_t* page_v = page_k + p.c_skv;
     const uint16_t* src = p.v + int64_t(tok) * p.v_st;
-    for (int u = threadIdx.x; u < p.hkv * (kHeadDim / 8); u += blockDim.x) {
-      const int h = u / (kHeadDim / 8), c8 = (u % (kHeadDim / 8)) * 8;
-      *reinterpret_cast<uint4*>(page_v + int64_t(h) * p.c_sh + c8) =
-          *reinterpret_cast<const uint4*>(src + int64_t(h) * p.v_sh + c8);
-    }
+    *reinterpret_cast<uint4*>(page_v + int64_t(h) * p.c_sh + lane * 8) =
+        *reinterpret_cast<const uint4*>(src + int64_t(h) * p.v_sh + lane * 8);
   }
 }
 
@@ -208,7 +211,9 @@ extern "C" int aspire_qk_norm_rope_append(const aspire_rope_args* a, void* strea
     ASPIRE_CHECK_ARG(a->v == nullptr || (aligned(a->v, 16) && a->v_stride_t % 8 == 0 && a->v_stride_h % 8 == 0),
                      "v rows must be 16-byte aligned");
   }
-  hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(a->total_tokens), dim3(256), 0,
+  const int head_blocks = (std::max(a->num_qo_heads + a->num_kv_heads, a->num_kv_heads) + kHeadsPerBlock - 1) /
+                          kHeadsPerBlock;
+  hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(a->total_tokens, head_blocks), dim3(256), 0,
                      static_cast<hipStream_t>(stream), p);
   ASPIRE_CHECK_LAUNCH();
   return ASPIRE_OK;
