@@ -35,7 +35,9 @@ def _mark_static(t: torch.Tensor) -> None:
 
 
 class KVCache(nn.Module):
-    """One buffer for target and draft pages; ``kv_cache`` / ``draft_cache`` are views into it."""
+    """The paged cache of one layer. With ``spec`` a single allocation holds the target
+    pages followed by the draft pages, and ``kv_cache`` / ``draft_cache`` slice it
+    (no second buffer); otherwise ``kv_cache`` is the whole allocation."""
 
     def __init__(self, max_num_pages: int, page_size: int, n_heads: int, head_dim: int,
                  dtype: torch.dtype = torch.bfloat16, spec: bool = False, draft_max_num_pages: int = 0,
@@ -89,7 +91,7 @@ def static_block_table(max_batch_size: int, max_seq_length: int, page_size: int,
 def graph_buckets(max_tokens: int) -> tuple[int, ...]:
     """Token counts graphs are captured for: 1, 2, 4, then every multiple of 8, and max_tokens."""
     if max_tokens < 1:
-        raise ValueError("max_tokens must be positive")
+        raise ValueError(f"graph_buckets needs at least one token, got max_tokens={max_tokens}")
     sizes = {s for s in (1, 2, 4) if s <= max_tokens}
     sizes.update(range(8, max_tokens + 1, 8))
     sizes.add(max_tokens)
@@ -99,11 +101,11 @@ def graph_buckets(max_tokens: int) -> tuple[int, ...]:
 def select_bucket(tokens: int, buckets: tuple[int, ...]) -> int:
     """The smallest bucket that holds ``tokens``."""
     if tokens < 1:
-        raise ValueError("tokens must be positive")
+        raise ValueError(f"select_bucket needs at least one token, got {tokens}")
     for b in buckets:
         if tokens <= b:
             return b
-    raise ValueError(f"{tokens} tokens exceed largest graph bucket {buckets[-1]}")
+    raise ValueError(f"no graph bucket holds {tokens} tokens (the largest is {buckets[-1]})")
 
 
 __all__ = ["KVCache", "get_num_pages", "get_last_page_len", "static_block_table", "graph_buckets",

@@ -26,7 +26,9 @@ _FULL_KINDS = {None: 0, "mirror": 1, "effective_full": 2}
 
 @dataclass(frozen=True)
 class HostPlanConfig:
-    """Backend facts the mirror needs to reproduce the device plan arrays."""
+    """Static settings of the attention backend (page size, batch capacity, draft-table
+    refresh family, dump-wrapper layout, selection budgets) that fix how each step's
+    plan arrays are rendered."""
 
     page_size: int
     max_batch: int
@@ -60,7 +62,8 @@ def _p(a) -> ctypes.c_void_p:
 
 
 class HostPlanState:
-    """Host-side twin of the backend's length/page bookkeeping (host_plan.py:59-306).
+    """Per-row length and page-count state kept on the host, advanced once per decode
+    step so the plan arrays never need a device readback (host_plan.py:59-306).
 
     The plan tensors and the per-row / per-token arrays ``build_step`` returns
     are views of buffers this object owns (allocated once, as the reference

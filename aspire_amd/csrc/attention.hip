@@ -695,8 +695,9 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
   ASPIRE_CHECK_ARG(a->head_dim == kHeadDim, "head_dim must be 128");
   ASPIRE_CHECK_ARG(a->page_size == kPage, "page_size must be 16");
   ASPIRE_CHECK_ARG(a->num_kv_heads > 0 && a->num_kv_heads < 256 &&
-                       a->num_qo_heads % a->num_kv_heads == 0,
-                   "bad head counts");
+                       a->num_qo_heads % a->num_kv_heads == 0 &&
+                       a->num_qo_heads / a->num_kv_heads <= 16 * kMaxRowTiles,
+                   "bad head counts (num_qo_heads a multiple of num_kv_heads, group at most 48)");
   ASPIRE_CHECK_ARG(a->q && a->kv_cache && a->kv_indices && a->out && a->plan_dev && a->float_ws,
                    "null pointer");
   ASPIRE_CHECK_ARG(al16(a->q) && al16(a->kv_cache) && al16(a->out) && al16(a->float_ws),

@@ -318,6 +318,8 @@ int check_common(const aspire_plan_layout* layout, const int32_t* qo_indptr, int
   else if (page_size != kPage) msg = "page_size must be 16";
   else if (num_kv_heads <= 0 || num_kv_heads >= 256) msg = "num_kv_heads must be in [1, 255]";
   else if (num_qo_heads <= 0 || num_qo_heads % num_kv_heads != 0) msg = "num_qo_heads must be a multiple of num_kv_heads";
+  // a query token's GQA group is the smallest row unit: it must fit one 3-tile item
+  else if (num_qo_heads / num_kv_heads > 16 * kMaxRowTiles) msg = "num_qo_heads / num_kv_heads must be at most 48";
   else if (host_buf_bytes < plan_offsets(*layout).total * 4) msg = "host plan buffer smaller than the layout";
   if (msg) {
     set_error("%s: %s", fn, msg);

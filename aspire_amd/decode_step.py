@@ -222,6 +222,14 @@ class MixedDecodeStep:
             raise ValueError("head_dim 128 and whole GQA groups only")
         if not 0 <= refresh_layer < shape.n_layer:
             raise ValueError("refresh_layer must be one of the model's layers")
+        # A draft segment's length is (count - 1) * 16 + last_page_len: the row's current
+        # (partial) page must be the last entry of every selection, which only a forced
+        # recent page guarantees.
+        if recent_pages < 1:
+            raise ValueError("recent_pages must be >= 1 (the current page ends every draft list)")
+        # The refresh layer scores pages of whole rows; a row cut into query tiles has none.
+        if np.any(ql * (shape.n_head // shape.n_local_heads) > 48):
+            raise ValueError("q_len * (n_head / n_local_heads) must be at most 48 for every row")
         if caches.shape[1:] != (caches.shape[1], 2, PAGE, shape.n_local_heads, shape.head_dim) \
                 or caches.shape[0] != shape.n_layer or caches.dtype != torch.bfloat16:
             raise ValueError("caches must be [n_layer, P, 2, 16, H_kv, 128] bf16")

@@ -7,7 +7,7 @@ and base-2 log-sum-exp ``lse_c``,
 
     lse = log2(sum_c 2^lse_c),   o = sum_c 2^(lse_c - lse) * o_c.
 
-Pinned by ``tests/test_oracle_merge.py``: splitting a row's keys into chunks,
+Pinned by ``tests/test_oracle_attention.py`` (the merge tests): splitting a row's keys into chunks,
 attending each chunk with ``oracle.attention`` and merging reproduces the
 unsplit attention (a closed-form identity); merging one chunk is the identity;
 a chunk with ``lse = -inf`` contributes nothing.

@@ -14,10 +14,14 @@ nothing from the reference source is copied.
 
 from __future__ import annotations
 
-import importlib.util
-import math
 import sys
-from pathlib import Path
+
+# Loading the reference module must leave nothing in its tree: no __pycache__.
+sys.dont_write_bytecode = True
+
+import importlib.util  # noqa: E402
+import math  # noqa: E402
+from pathlib import Path  # noqa: E402
 
 import numpy as np
 import torch

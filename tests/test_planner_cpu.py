@@ -268,3 +268,22 @@ def test_segments_shared_and_per_head_rows():
         bad = pages.copy()
         bad[5] -= 1
         plan_segments(lay, qo, start, bad, kvl, hq, hkv)
+
+
+def test_rejects_gqa_group_wider_than_three_tiles():
+    """A query token's GQA group must fit one 3-tile item (48 rows): 64 q heads over one
+    kv head is refused with ASPIRE_ERR_INVALID instead of planned past the last class."""
+    lay = layout(num_cus=16, waves_per_cu=4)
+    qo = np.array([0, 1], dtype=np.int32)
+    kvp = np.array([0, 4], dtype=np.int32)
+    kvl = np.array([64], dtype=np.int32)
+    buf = np.zeros(8 << 18, dtype=np.int32)
+    info = _lib.PlanInfo()
+    rc = _lib.lib().aspire_plan_build(
+        ctypes.byref(lay), qo.ctypes.data_as(ctypes.c_void_p), kvp.ctypes.data_as(ctypes.c_void_p),
+        kvl.ctypes.data_as(ctypes.c_void_p), 1, 0, 64, 1, 16, 1, buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes,
+        ctypes.byref(info))
+    assert rc == _lib.ASPIRE_ERR_INVALID
+    assert "at most 48" in _lib.lib().aspire_last_error().decode()
+    # the widest accepted group (48 q heads per kv head) still plans
+    plan(lay, qo, kvp, kvl, 48, 1)
