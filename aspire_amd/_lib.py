@@ -42,7 +42,11 @@ EXPORTED = (
     "aspire_add_rms_norm",
     "aspire_silu_mul",
     "aspire_argmax_rows",
+    "aspire_attention_run_static",
 )
+
+# Bytes of the static device scratch behind aspire_attention_run_static (ASPIRE_STATIC_SCRATCH_BYTES).
+STATIC_SCRATCH_BYTES = 64 << 20
 
 
 class PlanLayout(ctypes.Structure):
@@ -163,6 +167,7 @@ def _declare(lib):
                               ctypes.POINTER(PlanInfo)],
         "aspire_plan_upload": [ctypes.POINTER(PlanLayout), ctypes.POINTER(PlanInfo), vp, vp, vp],
         "aspire_attention_run": [ctypes.POINTER(PlanLayout), ctypes.POINTER(AttentionArgs), vp],
+        "aspire_attention_run_static": [ctypes.POINTER(PlanLayout), ctypes.POINTER(AttentionArgs), vp],
         "aspire_merge_states": [vp, vp, i32, i64, i32, vp, i32, vp, vp],
         "aspire_select_first_last_scores": [vp, i64, i32, i32, i32, vp, i32, vp, vp, vp, i32, i32, f32, vp, i64,
                                             i32, vp],  # ..., scores, score_stride, slots, stream

@@ -21,6 +21,7 @@
 //     reduced across the 4 lane groups with permlane swaps (no LDS).
 // A row tile is 16 query rows; NT tiles share the K/V registers
 // (q_len * group <= 16 * NT). One persistent launch runs every class.
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -688,19 +689,46 @@ inline bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 1
 }  // namespace
 }  // namespace aspire
 
-extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
-                                    const aspire_attention_args* a, void* stream) {
-  using namespace aspire;
-  ASPIRE_CHECK_ARG(layout && a, "null argument");
+// Split-KV partials of aspire_attention_run_static: a file-scope device array
+// of ASPIRE_STATIC_SCRATCH_BYTES that every GPU the library runs on holds until
+// the process ends. In host code `scratch` names the host-side shadow, not
+// device memory: its device address comes from hipGetSymbolAddress, once per
+// device (static_scratch_ptr), and only that address reaches kernels.
+static __device__ __align__(256) float scratch[ASPIRE_STATIC_SCRATCH_BYTES / sizeof(float)];
+
+namespace aspire {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // per device, guarded by g_scratch_mu
+
+// Device address of `scratch` on device dev (the current device).
+int static_scratch_ptr(int dev, float** out) {
+  ASPIRE_CHECK_ARG(dev >= 0 && dev < kMaxScratchDevices, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    ASPIRE_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    ASPIRE_CHECK_ARG(ptr != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<float*>(g_scratch_ptr[dev]);
+  return ASPIRE_OK;
+}
+
+// Shared body of both entry points: the partials live at float_ws.
+int attention_run_impl(const aspire_plan_layout* layout, const aspire_attention_args* a, float* float_ws,
+                       void* stream) {
   ASPIRE_CHECK_ARG(a->head_dim == kHeadDim, "head_dim must be 128");
   ASPIRE_CHECK_ARG(a->page_size == kPage, "page_size must be 16");
   ASPIRE_CHECK_ARG(a->num_kv_heads > 0 && a->num_kv_heads < 256 &&
                        a->num_qo_heads % a->num_kv_heads == 0 &&
                        a->num_qo_heads / a->num_kv_heads <= 16 * kMaxRowTiles,
                    "bad head counts (num_qo_heads a multiple of num_kv_heads, group at most 48)");
-  ASPIRE_CHECK_ARG(a->q && a->kv_cache && a->kv_indices && a->out && a->plan_dev && a->float_ws,
+  ASPIRE_CHECK_ARG(a->q && a->kv_cache && a->kv_indices && a->out && a->plan_dev && float_ws,
                    "null pointer");
-  ASPIRE_CHECK_ARG(al16(a->q) && al16(a->kv_cache) && al16(a->out) && al16(a->float_ws),
+  ASPIRE_CHECK_ARG(al16(a->q) && al16(a->kv_cache) && al16(a->out) && al16(float_ws),
                    "q, kv_cache, out and the float workspace must be 16-byte aligned");
   ASPIRE_CHECK_ARG(a->q_stride_t % 8 == 0 && a->q_stride_h % 8 == 0 && a->out_stride_t % 8 == 0 &&
                        a->out_stride_h % 8 == 0 && a->cache_stride_p % 8 == 0 &&
@@ -730,8 +758,8 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
   p.lse = a->lse;
   p.plan = static_cast<const int32_t*>(a->plan_dev);
   p.num_waves = layout->num_waves;
-  p.part_o = a->float_ws;
-  p.part_lse = a->float_ws + layout->partial_rows_cap * kHeadDim;
+  p.part_o = float_ws;
+  p.part_lse = float_ws + layout->partial_rows_cap * kHeadDim;
   p.hq = a->num_qo_heads;
   p.hkv = a->num_kv_heads;
   p.group = a->num_qo_heads / a->num_kv_heads;
@@ -776,6 +804,45 @@ extern "C" int aspire_attention_run(const aspire_plan_layout* layout,
     ASPIRE_CHECK_LAUNCH();
   }
   return ASPIRE_OK;
+}
+
+}  // namespace
+}  // namespace aspire
+
+extern "C" int aspire_attention_run(const aspire_plan_layout* layout, const aspire_attention_args* a,
+                                    void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(layout && a, "null argument");
+  return attention_run_impl(layout, a, a->float_ws, stream);
+}
+
+extern "C" int aspire_attention_run_static(const aspire_plan_layout* layout, const aspire_attention_args* a,
+                                           void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(layout && a, "null argument");
+  ASPIRE_CHECK_ARG(a->float_ws == nullptr, "float_ws must be NULL: the partials live in the library's static array");
+  // The plan's partial rows are bounded by the layout's capacity; the layout
+  // must not describe more float workspace than the static array holds.
+  if (layout->float_ws_bytes > int64_t(ASPIRE_STATIC_SCRATCH_BYTES) || layout->partial_rows_cap < 0 ||
+      layout->partial_rows_cap * int64_t(kHeadDim + 1) * 4 > int64_t(ASPIRE_STATIC_SCRATCH_BYTES)) {
+    set_error("aspire_attention_run_static: the layout's float workspace (%lld bytes, %lld partial rows) exceeds "
+              "the static scratch of %lld bytes; build the layout with float_ws_bytes <= ASPIRE_STATIC_SCRATCH_BYTES",
+              static_cast<long long>(layout->float_ws_bytes), static_cast<long long>(layout->partial_rows_cap),
+              static_cast<long long>(ASPIRE_STATIC_SCRATCH_BYTES));
+    return ASPIRE_ERR_CAPACITY;
+  }
+  // The scratch address is per device: the stream must run on the current device.
+  int dev = -1;
+  ASPIRE_CHECK_HIP(hipGetDevice(&dev));
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    ASPIRE_CHECK_HIP(hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev));
+    ASPIRE_CHECK_ARG(sdev == dev, "the stream belongs to another device than the current one");
+  }
+  float* ws = nullptr;
+  const int rc = static_scratch_ptr(dev, &ws);
+  if (rc != ASPIRE_OK) return rc;
+  return attention_run_impl(layout, a, ws, stream);
 }
 
 extern "C" int aspire_merge_states(const float* v, const float* s, int32_t num_states, int64_t rows,

@@ -215,6 +215,25 @@ typedef struct aspire_attention_args {
 int aspire_attention_run(const aspire_plan_layout* layout,
                          const aspire_attention_args* args, void* stream);
 
+/* Size of the static device scratch of aspire_attention_run_static (bytes per
+ * GPU): 64 MiB, room for 130,055 fp32 partial rows. */
+#define ASPIRE_STATIC_SCRATCH_BYTES (64u << 20)
+
+/* aspire_attention_run without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as aspire_attention_run, except that
+ * args->float_ws must be NULL: the split-KV partials live in a static device
+ * array of ASPIRE_STATIC_SCRATCH_BYTES that each GPU the library runs on holds
+ * until the process ends. The layout must have been built with
+ * float_ws_bytes <= ASPIRE_STATIC_SCRATCH_BYTES (ASPIRE_ERR_CAPACITY
+ * otherwise), so every plan built from it fits. The stream must belong to the
+ * current device. Nothing needs clearing between calls (every partial row the
+ * merge reads is written first), but all calls on one GPU share the array:
+ * calls that overlap on one GPU (two streams, or two host threads) race. */
+int aspire_attention_run_static(const aspire_plan_layout* layout,
+                                const aspire_attention_args* args, void* stream);
+
 /* ---------------------------------------------------------------- (a6) -- */
 /* Standalone merge of num_states partial states (FlashInfer merge_states
  * semantics, base-2 lse): v [num_states, rows, head_dim] fp32, s
