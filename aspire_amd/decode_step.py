@@ -365,8 +365,10 @@ class MixedDecodeStep:
     def forward(self, capture: dict | None = None) -> torch.Tensor:
         """One decode step; returns the greedy token ids ``[T]`` (int64, device).
 
-        ``capture`` (a dict, for tests) receives each layer's attention input q
-        (after RoPE) as ``q{layer}`` and the final hidden state as ``h``."""
+        ``capture`` (a dict, for tests) receives each layer's fused projection
+        output before the q/k preparation as ``qkv{layer}``, the attention input q
+        (after RoPE) as ``q{layer}``, the attention output as ``y{layer}`` and the
+        final hidden state as ``h``."""
         s, w = self.shape, self.w
         T = self.T
         qs, kvs = s.q_size, s.kv_size
@@ -379,12 +381,16 @@ class MixedDecodeStep:
             q = qkv[:, :qs].view(T, s.n_head, s.head_dim)
             k = qkv[:, qs : qs + kvs].view(T, s.n_local_heads, s.head_dim)
             v = qkv[:, qs + kvs :].view(T, s.n_local_heads, s.head_dim)
+            if capture is not None:
+                capture[f"qkv{layer}"] = qkv.clone()  # q is rewritten in place below
             qk_norm_rope_update_kv(q, k, v, lw["q_norm"], lw["k_norm"], s.norm_eps, self.qo_indptr, self.offsets,
                                    self.caches[layer], self.full_indices, self.full_indptr, self.last_page_len, PAGE,
                                    config=self.rope)
             if capture is not None:
                 capture[f"q{layer}"] = q.clone()
             self.attention(layer, q)
+            if capture is not None:
+                capture[f"y{layer}"] = self.y.clone()
             attn_out = F.linear(self.y.view(T, qs), lw["wo"])
             add_rms_norm(self.x, lw["ffn_norm"], self.a, s.norm_eps, delta=attn_out)
             gate_up = F.linear(self.a, lw["w13"])

@@ -127,11 +127,13 @@ def paged_attention(
                 if enabled:
                     _write_dump(dump, b, heads, s, qlen, n)
             if page_scores is not None and qlen == 1 and n > 0:
+                # page j's key mean over its valid keys (the last page may be partial)
                 npages = (n + 15) // 16
-                for j in range(npages):
-                    t0, t1 = j * 16, min((j + 1) * 16, n)
-                    kmean = kg[t0:t1].mean(dim=0)
-                    page_scores[b * num_kv_heads + g, j] = (qs[0] @ kmean).max()
+                padded = torch.cat([kg, kg.new_zeros(npages * 16 - n, d)]) if npages * 16 > n else kg
+                count = torch.full((npages, 1), 16.0, dtype=compute_dtype)
+                count[-1] = n - (npages - 1) * 16
+                kmean = padded.view(npages, 16, d).sum(dim=1) / count
+                page_scores[b * num_kv_heads + g, :npages] = (qs[0] @ kmean.T).amax(dim=0).to(page_scores.dtype)
             x = s * (sm_scale * LOG2E)
             if causal and n > 0:
                 i_idx = torch.arange(qlen).view(1, qlen, 1)

@@ -53,3 +53,22 @@ def assert_topk_sets(selected_logical, scores, k, tol=1e-3):
     must_not = set(np.flatnonzero(s < t - tol).tolist()) if np.isfinite(t) else set(np.flatnonzero(s < t).tolist())
     assert must <= got, f"missing pages {sorted(must - got)[:10]}"
     assert not (got & must_not), f"extra pages {sorted(got & must_not)[:10]}"
+
+
+def oracle_row(q: torch.Tensor, cache: torch.Tensor, tokens, page_lists, kv_lens, num_kv_heads: int,
+               per_head: bool = False, **kw):
+    """CPU oracle for one row whose pages are gathered on the device first (only the row's
+    pages cross to the host). ``page_lists``: the row's physical page list, or with
+    ``per_head`` one list per kv head (``kv_lens`` then per head); ``tokens``: the row's token
+    indices into ``q``. Returns ``(out [t, H_q, D], lse [t, H_q])``; extra keywords go to the
+    oracle."""
+    from oracle.attention import paged_attention
+
+    lists = [torch.as_tensor(np.asarray(p), dtype=torch.int64) for p in (page_lists if per_head else [page_lists])]
+    used = torch.cat(lists)
+    uniq, inv = torch.unique(used, return_inverse=True)
+    small = cache[uniq.to(cache.device)].cpu()
+    kvp = np.concatenate([[0], np.cumsum([len(x) for x in lists])])
+    toks = list(tokens)
+    return paged_attention(q[toks].cpu(), small, [0, len(toks)], kvp, inv.to(torch.int32),
+                           [int(x) for x in kv_lens], num_kv_heads=num_kv_heads, per_head_lists=per_head, **kw)

@@ -105,23 +105,30 @@ def test_head_page_lists(gpu, share):
 
 SMALL = ModelShape(n_layer=4, dim=512, n_head=8, n_local_heads=2, head_dim=128, intermediate_size=1024,
                    vocab_size=1024, rope_base=1e6)
+# Qwen3-8B's attention shape (32 q / 8 kv heads, GQA 4) on a small model: 8 kv heads per slot put the
+# verify rows' shared lists on the staged LDS path, with the draft rows' per-head lists direct, in one
+# launch (the mix the full decode step runs)
+SMALL_GQA4 = ModelShape(n_layer=4, dim=512, n_head=32, n_local_heads=8, head_dim=128, intermediate_size=1024,
+                        vocab_size=1024, rope_base=1e6)
+SHAPES = [pytest.param(SMALL, id="gqa4_hkv2"), pytest.param(SMALL_GQA4, id="gqa4_hkv8")]
 
 
-def _small_step(gpu, budget=8, seed=0):
+def _small_step(gpu, budget=8, seed=0, shape=SMALL):
     ctx = np.array([700, 1500, 333, 1200, 260, 980])
     ql = np.array([1, 2, 1, 5, 1, 9])                  # verify rows fill 8, 20 and 36 query rows
     dr = ql == 1
     n_pages = (ctx + 15) // 16
     table, pool = random_block_table(n_pages, seed=seed, pool_pages=int(n_pages.sum()) + 11)
-    w = DecodeWeights(SMALL, gpu, seed=seed)
-    caches = alloc_kv_caches(SMALL, pool, gpu, seed=seed)
+    w = DecodeWeights(shape, gpu, seed=seed)
+    caches = alloc_kv_caches(shape, pool, gpu, seed=seed)
     step = MixedDecodeStep(w, caches, ctx, ql, dr, torch.from_numpy(table), budget=budget, refresh_layer=2)
     return step, ctx, ql, dr, table
 
 
-def test_small_decode_step_matches_oracle(gpu):
-    say("small decode step")
-    step, ctx, ql, dr, table = _small_step(gpu)
+@pytest.mark.parametrize("shape", SHAPES)
+def test_small_decode_step_matches_oracle(gpu, shape):
+    say("small decode step", shape)
+    step, ctx, ql, dr, table = _small_step(gpu, shape=shape)
     B, H = step.batch, step.heads
     init_sel = step.selector.selected.cpu().numpy().copy()
     init_cnt = step.selector.counts.cpu().numpy().copy()
@@ -129,6 +136,10 @@ def test_small_decode_step_matches_oracle(gpu):
     cap = {}
     ids = step.forward(capture=cap)
     torch.cuda.synchronize()
+    # the mixed layers ran one head-aligned plan: a slot is the row's n_local_heads waves
+    # (int 4 of the plan header), so with 8 kv heads the verify rows stage their shared pages
+    hpu = int(step.mixed_wrapper._int_workspace[16:20].view(torch.int32).item())
+    assert hpu == shape.n_local_heads
     sel = step.selector.selected.cpu().numpy()
     cnt = step.selector.counts.cpu().numpy()
     scores = step.selector.page_scores.cpu()
@@ -173,11 +184,12 @@ def test_small_decode_step_matches_oracle(gpu):
     assert int(changed.sum()) <= step.shape.n_layer * int(((ctx - 1) // 16 - (ctx - ql) // 16 + 1).sum())
 
 
-def test_decode_step_graph_replays_match_eager(gpu):
+@pytest.mark.parametrize("shape", SHAPES)
+def test_decode_step_graph_replays_match_eager(gpu, shape):
     """The whole step recorded in one HIP graph: every replay equals the eager step from the
     same state (the draft selection carried from step to step), with eager work between."""
-    say("decode step graph")
-    step, *_ = _small_step(gpu, budget=6, seed=3)
+    say("decode step graph", shape)
+    step, *_ = _small_step(gpu, budget=6, seed=3, shape=shape)
     state = [step.selector.selected, step.selector.counts, step.mixed_indices, step.mixed_indptr]
     saved = [t.clone() for t in state]
 

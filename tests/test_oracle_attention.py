@@ -138,3 +138,42 @@ def test_dump_layout_first_last():
     assert torch.isinf(view[b, :, :, lens[b]:]).all()
     # single-query row writes slot 0 only
     assert torch.isinf(view[0, :, 1]).all()
+
+
+def test_keymean_page_scores_closed_forms():
+    """The key-mean page score of a single-query row: with every valid key of page j equal
+    to c_j the score is max_h q_h . c_j; a partial last page averages only its valid keys
+    (the slots past kv_len hold large values that would show if they were counted); rows
+    with more than one query leave their scores untouched."""
+    g = torch.Generator().manual_seed(8)
+    D, hq, hkv, page = 16, 4, 2, 16
+    lens = [16 * 3 + 5, 32, 20]          # row 0: partial last page of 5 keys; row 2 has 3 queries
+    qlens = [1, 1, 3]
+    P = 10
+    cache = torch.zeros(P, 2, page, hkv, D, dtype=torch.bfloat16)
+    consts = torch.randn(P, hkv, D, generator=g).to(torch.bfloat16)
+    cache[:, 0] = consts[:, None]
+    pages = [[3, 7, 1, 5], [0, 9], [2, 4]]
+    # row 0's last page (5): 5 distinct valid keys, large values in the 11 slots past kv_len
+    valid = torch.randn(5, hkv, D, generator=g).to(torch.bfloat16)
+    cache[5, 0, :5] = valid
+    cache[5, 0, 5:] = 1000.0
+    kvp = [0, 4, 6, 8]
+    kvi = torch.tensor(sum(pages, []), dtype=torch.int32)
+    qo = [0, 1, 2, 5]
+    q = torch.randn(5, hq, D, generator=g).to(torch.bfloat16)
+    scores = torch.full((3 * hkv, 8), float("nan"))
+    paged_attention(q, cache, qo, kvp, kvi, lens, num_kv_heads=hkv, page_scores=scores)
+    group = hq // hkv
+    for b in (0, 1):
+        for kvh in range(hkv):
+            qh = q[qo[b], kvh * group : (kvh + 1) * group].double()
+            for j, p in enumerate(pages[b]):
+                if b == 0 and j == 3:
+                    c = valid[:, kvh].double().mean(dim=0)       # only the 5 valid keys
+                else:
+                    c = consts[p, kvh].double()
+                want = float((qh @ c).max())
+                assert abs(float(scores[b * hkv + kvh, j]) - want) <= 1e-4 * (1 + abs(want)), (b, kvh, j)
+            assert torch.isnan(scores[b * hkv + kvh, len(pages[b]):]).all()
+    assert torch.isnan(scores[2 * hkv :]).all()          # 3 queries: no scores
