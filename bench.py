@@ -15,9 +15,11 @@ top-128 page selection).
 value = algorithmic HBM bytes of the step / step time (GB/s). The roofline
 object reports the dominant kernel (mixed attention) alone: its algorithmic
 bytes per launch (KV pages read + q + o + page ids) over its average launch
-time, measured with HIP events on the stream it runs on. The CPU baseline
-times the repository's CPU oracle (torch fp32) on a bounded sample of rows of
-the same workload on the host cores.
+time, measured with HIP events on the stream it runs on. Before the warm-up
+steps an untimed clock-settle phase runs the step back to back for
+--prewarm-ms (reported). The CPU baseline times the repository's CPU oracle
+(torch fp32) on the host cores: configs 0 and 1 whole, config 2 on 16 of its
+64 rows, each the median of 5 runs after 2 warm-ups.
 """
 
 from __future__ import annotations
@@ -25,6 +27,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -68,13 +71,16 @@ def parse():
                          "step); 2: refresh layer; 3: the full 36-layer decode step alone")
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-runs", type=int, default=5, help="timed CPU-baseline runs per config (after 2 warm-ups)")
     ap.add_argument("--no-components", action="store_true",
                     help="skip the per-component measurements (append, page list, merge, selectors, refresh layer)")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 full decode step")
     ap.add_argument("--decode-steps", type=int, default=30, help="timed graph replays of the config-3 step")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (read + write) for rocprofv3 counter calibration")
+    ap.add_argument("--prewarm-ms", type=float, default=1000.0,
+                    help="untimed clock-settle phase before the warm-up steps: the step runs back to back for "
+                         "this long (wall clock), reported as config.timing.prewarm_ms")
     return ap.parse_args()
 
 
@@ -88,6 +94,43 @@ def timed(fn, steps, stream):
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps  # ms
+
+
+def timed_steps(fn, steps, stream):
+    """Time ``steps`` back-to-back calls with one HIP event between consecutive calls (on
+    ``stream``, where every kernel of the step launches). Returns (mean ms, per-call ms list):
+    the mean is first-event-to-last-event over the calls."""
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for i in range(steps):
+        fn()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return ev[0].elapsed_time(ev[steps]) / steps, per
+
+
+def prewarm(fn, ms):
+    """Run ``fn`` back to back for ``ms`` of wall clock (GPU clocks ramp up over the first tens
+    of milliseconds of sustained work after an idle period). Returns (wall ms, calls)."""
+    if ms <= 0:
+        return 0.0, 0
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            fn()
+        n += 10
+        torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3, n
+
+
+def summary(per):
+    a = np.asarray(per, dtype=np.float64)
+    return {"median_ms": round(float(np.median(a)), 5), "mean_ms": round(float(a.mean()), 5),
+            "p10_ms": round(float(np.percentile(a, 10)), 5), "p90_ms": round(float(np.percentile(a, 90)), 5),
+            "min_ms": round(float(a.min()), 5), "max_ms": round(float(a.max()), 5)}
 
 
 def graph_timed(fn, steps, stream, reps=20, warm=2):
@@ -139,23 +182,6 @@ def attention_only(w, q, cache, out, class_mask=None):
         _lib.check(rc, "attention_only")
 
     return launch
-
-
-def cpu_baseline(step_cpu_fn, budget_s):
-    """Time the CPU oracle on rows until ``budget_s`` of work; returns (GB/s, bytes, seconds, rows)."""
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    done_bytes, t_total, rows = 0, 0.0, []
-    for row, fn, nbytes in step_cpu_fn():
-        t0 = time.perf_counter()
-        fn()
-        dt = time.perf_counter() - t0
-        done_bytes += nbytes
-        t_total += dt
-        rows.append(row)
-        if t_total >= budget_s:
-            break
-    return done_bytes / t_total / 1e9, done_bytes, t_total, rows, threads
 
 
 def main():
@@ -226,22 +252,24 @@ def main():
                                              step.kv_indptr, step.last_page_len, PAGE)
             w.run(step.q, cache, out=out)
 
+    pw_ms, pw_steps = prewarm(run_step, args.prewarm_ms)
     for _ in range(args.warmup):
         run_step()
     torch.cuda.synchronize()
-    log(f"timing {args.steps} steps")
-    ms = timed(run_step, args.steps, stream)
+    log(f"clock settle {pw_ms:.0f} ms ({pw_steps} steps), {args.warmup} warm-up steps; timing {args.steps} steps")
+    ms, per_step = timed_steps(run_step, args.steps, stream)
     value = nbytes["total"] / (ms * 1e-3) / 1e9
 
     # dominant kernel alone: mixed attention (no merge), same plan, same stream
     attn = attention_only(w, step.q, cache, out)
     for _ in range(3):
         attn()
-    attn_ms = timed(attn, args.steps, stream)
+    attn_ms, attn_per = timed_steps(attn, args.steps, stream)
     attn_bytes = nbytes["kv"] + nbytes["qo"] + nbytes["indices"]
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
-    log(f"step {ms * 1e3:.1f} us -> {value:.0f} GB/s; attention kernel {attn_ms * 1e3:.1f} us -> "
-        f"{achieved:.0f} GB/s ({achieved / PEAK_HBM_GBS:.1%} of 8 TB/s)")
+    log(f"step {ms * 1e3:.1f} us (median {np.median(per_step) * 1e3:.1f}) -> {value:.0f} GB/s; attention kernel "
+        f"{attn_ms * 1e3:.1f} us (median {np.median(attn_per) * 1e3:.1f}) -> {achieved:.0f} GB/s "
+        f"({achieved / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
     if args.calibrate_copy:
         src = torch.empty(1 << 29, dtype=torch.int16, device=dev).random_()
@@ -262,7 +290,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = run_cpu_baseline(step, args.cpu_seconds)
+        cpu = run_cpu_baseline(step, args.config, args.cpu_runs)
 
     tokens = step.total_tokens
     if args.config == 1:
@@ -297,6 +325,11 @@ def main():
             "decode_tokens_per_s_layer": round(tokens / (ms * 1e-3), 1),
             "plan_host_us": round(plan_us, 1),
             "plan": {"items": list(info.num_items), "merges": info.num_merge, "waves": w._layout.num_waves},
+            "timing": {"prewarm_ms": round(pw_ms, 1), "prewarm_steps": pw_steps,
+                       "note": "untimed clock-settle phase (the step back to back) before the warm-up steps; "
+                               "ms_per_step is the mean over the timed steps (first to last HIP event), "
+                               "per_step the distribution of the per-step events",
+                       "per_step": summary(per_step), "attention_kernel": summary(attn_per)},
         },
         "roofline": {
             "bound": "hbm",
@@ -616,10 +649,11 @@ def measure_config3(steps, warmup, waves_per_cu):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step.forward()
+    pw_ms, _ = prewarm(graph.replay, 500)
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
-    ms = timed(graph.replay, steps, stream)
+    ms, per_step = timed_steps(graph.replay, steps, stream)
     attn_graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(attn_graph):
         step.attention_only()
@@ -650,60 +684,131 @@ def measure_config3(steps, warmup, waves_per_cu):
         "attention_kv_gbs": round(attn_gbs, 1),
         "plan_host_us": round(plan_us, 1),
         "verify_q_len": ql[~dr].tolist(),
+        "timing": {"prewarm_ms": round(pw_ms, 1), "per_step": summary(per_step)},
     }
     del graph, attn_graph, step, caches, weights
     torch.cuda.empty_cache()
     return res
 
 
-def run_cpu_baseline(step, budget_s):
-    """CPU oracle (append + attention, torch fp32) on rows of the same workload."""
+def _cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return "unknown"
+
+
+def _cpu_layer(step, rows, *, append: bool, select_k: int = 0):
+    """CPU inputs of one layer restricted to ``rows``: only their pages cross to the host (gathered
+    on the device, renumbered). Returns (fn, algorithmic bytes): fn runs the CPU oracle, the
+    paged append in place (``append``) then attention over every listed row, plus the key-mean
+    page scores and the top-``select_k`` pages per (row, kv head) when ``select_k``."""
+    from aspire_amd.workloads import PAGE
     from oracle.append import paged_kv_append
     from oracle.attention import paged_attention
+    from oracle.select import topk_pages_per_head
 
     qo = step.qo_indptr_host.numpy()
     kvp = step.kv_indptr_host.numpy()
     kvl = step.kv_len_host.numpy()
+    lpl = step.last_page_len.cpu().numpy()
     idx = step.kv_indices.cpu()
-    order = []
-    # alternate verify and draft rows (verify rows dominate the bytes)
-    ver = [b for b in range(step.batch) if not step.is_draft[b]]
-    dra = [b for b in range(step.batch) if step.is_draft[b]]
-    for i in range(max(len(ver), len(dra))):
-        order += ([ver[i]] if i < len(ver) else []) + ([dra[i]] if i < len(dra) else [])
+    lists = [idx[int(kvp[b]) : int(kvp[b + 1])].long() for b in rows]
+    uniq, inv = torch.unique(torch.cat(lists), return_inverse=True)
+    cache = step.cache[uniq.to(step.cache.device)].cpu()
+    cache_bits = cache.view(torch.int16).numpy()          # shares memory with ``cache``
+    sub_kvp = np.concatenate([[0], np.cumsum([len(x) for x in lists])]).astype(np.int64)
+    sub_idx = inv.to(torch.int32)
+    sub_idx_np = sub_idx.numpy()
+    toks = np.concatenate([np.arange(qo[b], qo[b + 1]) for b in rows]).astype(np.int64)
+    sub_qo = np.concatenate([[0], np.cumsum([qo[b + 1] - qo[b] for b in rows])]).astype(np.int64)
+    sub_kvl = [int(kvl[b]) for b in rows]
+    sub_lpl = np.array([int(lpl[b]) for b in rows], dtype=np.int64)
+    tok_d = torch.from_numpy(toks).to(step.q.device)
+    q = step.q[tok_d].cpu()
+    kn = step.k_new[tok_d].cpu().view(torch.int16).numpy()
+    vn = step.v_new[tok_d].cpu().view(torch.int16).numpy()
+    hkv = step.hkv
+    n_pages = np.repeat([(n + PAGE - 1) // PAGE for n in sub_kvl], hkv)
 
-    def rows():
-        for b in order:
-            pages = idx[kvp[b] : kvp[b + 1]].long()
-            small = step.cache[pages.to(step.cache.device)].cpu()
-            q = step.q[qo[b] : qo[b + 1]].cpu()
-            kn = step.k_new[qo[b] : qo[b + 1]].cpu()
-            vn = step.v_new[qo[b] : qo[b + 1]].cpu()
-            n_pages = int(kvp[b + 1] - kvp[b])
-            t = int(qo[b + 1] - qo[b])
-            local_idx = np.arange(n_pages, dtype=np.int32)
-            lpl = np.array([(int(kvl[b]) - 1) % 16 + 1], dtype=np.int32)
-            nbytes = int(kvl[b]) * step.hkv * 128 * 4 + t * step.hq * 128 * 4 + t * step.hkv * 128 * 8 + n_pages * 4
+    def fn():
+        if append:
+            paged_kv_append(kn, vn, sub_qo, cache_bits, sub_idx_np, sub_kvp, sub_lpl, PAGE, inplace=True)
+        scores = torch.full((len(rows) * hkv, int(n_pages.max())), float("nan")) if select_k else None
+        paged_attention(q, cache, sub_qo, sub_kvp, sub_idx, sub_kvl, num_kv_heads=hkv, page_scores=scores)
+        if select_k:
+            topk_pages_per_head(scores, n_pages, select_k, 0)
 
-            def fn(small=small, q=q, kn=kn, vn=vn, n_pages=n_pages, t=t, local_idx=local_idx, lpl=lpl, b=b):
-                cache_bits = small.view(torch.int16).numpy()
-                newc = paged_kv_append(kn.view(torch.int16).numpy(), vn.view(torch.int16).numpy(),
-                                       np.array([0, t]), cache_bits, local_idx, np.array([0, n_pages]), lpl, 16)
-                c = torch.from_numpy(newc).view(torch.bfloat16)
-                paged_attention(q, c, [0, t], [0, n_pages], torch.from_numpy(local_idx), [int(kvl[b])],
-                                num_kv_heads=step.hkv)
+    t = int(sub_qo[-1])
+    nbytes = (sum(sub_kvl) * hkv * 128 * 2 * 2 + t * step.hq * 128 * 2 * 2 + int(sub_kvp[-1]) * 4
+              + (t * hkv * 128 * 2 * 2 * 2 if append else 0) + (len(rows) * hkv * select_k * 4 if select_k else 0))
+    return fn, nbytes
 
-            yield b, fn, nbytes
 
-    gbs, done, secs, used, threads = cpu_baseline(rows, budget_s)
-    log(f"cpu baseline: {gbs:.2f} GB/s over {len(used)} rows in {secs:.1f}s on {threads} threads")
+def _cpu_time(fn, warmup: int, runs: int):
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), times
+
+
+def run_cpu_baseline(step, config: int, runs: int):
+    """The CPU oracle (torch fp32 attention, numpy append, key-mean scores and top-k) on the host
+    cores, per BASELINE.md's protocol: 2 warm-up runs, then the median of ``runs`` (>= 5) runs on
+    identical seeded inputs. Config 0 whole; config 1 whole (the bench workload: append +
+    attention); config 2 on a bounded sample of 16 of its 64 rows (attention + key-mean scores +
+    top-128), scaled to GB/s. Threads: the process's CPU share (OMP_NUM_THREADS, 16 on the GPU
+    boxes) capped by os.cpu_count(); both are reported."""
+    from aspire_amd.workloads import config0, config2
+
+    host_cpus = os.cpu_count() or 1
+    threads = min(host_cpus, int(os.environ.get("OMP_NUM_THREADS", host_cpus) or host_cpus))
+    torch.set_num_threads(threads)
+    dev = step.q.device
+    per = {}
+    t_all = time.perf_counter()
+
+    def measure(name, st, rows, **kw):
+        fn, nbytes = _cpu_layer(st, rows, **kw)
+        med, times = _cpu_time(fn, 2, max(runs, 5))
+        per[name] = {"median_s": round(med, 4), "runs_s": [round(x, 4) for x in times],
+                     "bytes": nbytes, "gbs": round(nbytes / med / 1e9, 3), "rows": len(rows)}
+        log(f"cpu baseline {name}: median {med * 1e3:.1f} ms over {len(times)} runs -> {nbytes / med / 1e9:.2f} GB/s")
+
+    c0 = config0(device=dev)
+    measure("config0", c0, list(range(c0.batch)), append=True)
+    del c0
+    main_name = f"config{config}"
+    measure(main_name, step, list(range(step.batch)), append=config == 1, select_k=128 if config == 2 else 0)
+    if config == 1:
+        c2 = config2(device=dev)
+        rng = np.random.default_rng(0)
+        measure("config2", c2, sorted(rng.choice(c2.batch, 16, replace=False).tolist()), append=False, select_k=128)
+        del c2
+        torch.cuda.empty_cache()
+    head = per[main_name]
     return {
-        "value": round(gbs, 3),
+        "value": head["gbs"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(used)} rows of the same workload (rows {used}), KV append + attention through the CPU "
-                  f"oracle (torch fp32), {done / 1e9:.2f} GB of algorithmic bytes in {secs:.1f} s",
+        "host_cpu_count": host_cpus,
+        "cpu_model": _cpu_model(),
+        "protocol": f"torch.set_num_threads({threads}); 2 warm-up runs, then the median of {max(runs, 5)} runs on "
+                    "identical seeded inputs; value = the bench workload's algorithmic bytes / median time",
+        "sample": f"{main_name}: the whole layer ({head['rows']} rows) through the CPU oracle"
+                  + (" (KV append + attention)" if config == 1 else " (attention + key-mean scores + top-128)")
+                  + "; config0: whole; config2: 16 of its 64 rows (attention + key-mean scores + top-128)",
+        "per_config": per,
+        "wall_s": round(time.perf_counter() - t_all, 1),
     }
 
 

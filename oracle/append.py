@@ -56,14 +56,17 @@ def paged_kv_append(
     kv_indptr: np.ndarray,
     last_page_len: np.ndarray,
     page_size: int,
+    *,
+    inplace: bool = False,
 ) -> np.ndarray:
-    """Return a copy of ``cache`` with the new K/V rows scattered in.
+    """Return a copy of ``cache`` with the new K/V rows scattered in (``inplace``:
+    scatter into ``cache`` itself and return it, as the reference mutates its cache).
 
     ``k``/``v``: ``[T, H_kv, D]`` (any dtype; bf16 is passed as its uint16
     bits); ``cache``: ``[P, 2, page_size, H_kv, D]`` of the same dtype. The skip
     rules are kv_ops.py:92-98 and the page/slot arithmetic kv_ops.py:100-103.
     """
-    out = cache.copy()
+    out = cache if inplace else cache.copy()
     total = k.shape[0]
     if total == 0:
         return out
