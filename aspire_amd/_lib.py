@@ -43,6 +43,11 @@ EXPORTED = (
     "aspire_silu_mul",
     "aspire_argmax_rows",
     "aspire_attention_run_static",
+    "aspire_topk_candidates",
+    "aspire_logits_pipe",
+    "aspire_sampling_from_probs",
+    "aspire_chain_speculative_sampling",
+    "aspire_verify_topk_speculation",
 )
 
 # Bytes of the static device scratch behind aspire_attention_run_static (ASPIRE_STATIC_SCRATCH_BYTES).
@@ -185,6 +190,11 @@ def _declare(lib):
         "aspire_add_rms_norm": [vp, i64, vp, i64, vp, vp, i64, i32, i32, f32, vp],
         "aspire_silu_mul": [vp, i64, vp, i64, i32, i32, vp],
         "aspire_argmax_rows": [vp, i64, i32, i32, vp, vp],
+        "aspire_topk_candidates": [vp, i64, i32, i32, i32, i64, vp, vp, vp],
+        "aspire_logits_pipe": [vp, i32, i64, i32, i32, f32, f32, vp, i64, vp],
+        "aspire_sampling_from_probs": [vp, i64, i32, i32, vp, vp, vp],
+        "aspire_chain_speculative_sampling": [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp],
+        "aspire_verify_topk_speculation": [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
     }
     for name, argtypes in sigs.items():
         fn = getattr(lib, name)

@@ -22,7 +22,7 @@ PKG = HERE.parent
 LIB = PKG / "libaspire_hip.so"
 BUILD = HERE / "_build"
 SOURCES = ["capi.cpp", "plan.cpp", "host_plan.cpp", "append.hip", "page_list.hip", "attention.hip", "select.hip",
-           "rope_append.hip", "decode_ops.hip"]
+           "rope_append.hip", "decode_ops.hip", "sampling.hip"]
 ARCH = "gfx950"
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function"]

@@ -1,0 +1,615 @@
+// (f4) Token sampling and speculative verification for gfx950.
+//
+// * topk_candidates_kernel: the top_k logits of a row and their ids, descending, ties to the
+//   lower id. Radix select on 16-bit order-preserving keys of the bf16 logits: a histogram of
+//   the high byte, then of the low byte among the boundary bin, gives the k-th key exactly;
+//   one ordered pass collects every larger key and the lowest-id ties; a bitonic sort in LDS
+//   orders the <= 1024 candidates. Histograms use 64 LDS sub-histograms (wave w, lane % 16)
+//   so lanes with equal keys rarely serialise on one counter.
+// * logits_pipe_kernel: temperature, softmax and top-p renormalisation of one row in LDS.
+// * sample_kernel / chain_kernel / verify_kernel: inverse-CDF draws with the uniforms given
+//   (a contiguous chunk per thread, chunk sums scanned in thread order, so the prefix sums
+//   are the same on every run), the chain speculative-sampling rule, and the reference's
+//   top-k verification fused around it (local vocabulary of top_k + 1 built on the fly).
+// One workgroup of 256 threads per row or request; these are per-token kernels (one decode
+// step samples at most a few hundred rows), latency- rather than bandwidth-bound.
+#include <cfloat>
+
+#include "common.h"
+
+namespace aspire {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxTopK = 1024;
+constexpr int kMaxPipeWidth = 4096;
+constexpr int kSubHists = kWaves * 16;
+
+// Order-preserving 16-bit key of a bf16 value; -0 and +0 share a key (they compare equal, so
+// they tie and fall back to the id order).
+__device__ __forceinline__ uint32_t bf16_key(uint16_t b) {
+  if (b == 0x8000u) b = 0;
+  return (b & 0x8000u) ? (~uint32_t(b) & 0xffffu) : (uint32_t(b) | 0x8000u);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_min_int(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_max_int(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// Block-wide reductions (256 threads); every thread gets the result.
+__device__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) s += red[w];
+  return s;
+}
+__device__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = -FLT_MAX;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) s = fmaxf(s, red[w]);
+  return s;
+}
+__device__ int block_min_int(int v, int* red) {
+  v = wave_min_int(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int s = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) s = min(s, red[w]);
+  return s;
+}
+__device__ int block_max_int(int v, int* red) {
+  v = wave_max_int(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int s = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) s = max(s, red[w]);
+  return s;
+}
+
+// Shared scratch of the draw: the per-thread chunk sums, scanned in thread order by one
+// thread (256 additions: the same association on every run).
+struct DrawLds {
+  float part[kThreads];
+  float excl[kThreads];
+  float total;
+  int ired[kWaves];
+  float fred[kWaves];
+};
+
+// Inverse-CDF draw over w(0..n-1) (weights >= 0, any scale): the first index whose inclusive
+// prefix sum exceeds u * sum(w); the last positive index if rounding leaves none; 0 if all are 0.
+// Thread t owns indices [t * chunk, (t + 1) * chunk). Every thread must call it.
+template <typename W>
+__device__ int block_draw(const W& w, int n, float u, DrawLds& s) {
+  const int t = threadIdx.x;
+  const int chunk = (n + kThreads - 1) / kThreads;
+  const int i0 = min(t * chunk, n), i1 = min(i0 + chunk, n);
+  float sum = 0.f;
+  int last_pos = -1;
+  for (int i = i0; i < i1; ++i) {
+    const float x = w(i);
+    sum += x;
+    if (x > 0.f) last_pos = i;
+  }
+  s.part[t] = sum;
+  __syncthreads();
+  if (t == 0) {
+    float acc = 0.f;
+    for (int j = 0; j < kThreads; ++j) {
+      s.excl[j] = acc;
+      acc += s.part[j];
+    }
+    s.total = acc;
+  }
+  __syncthreads();
+  const float target = u * s.total;
+  int hit = INT_MAX;
+  if (i0 < i1 && s.excl[t] + s.part[t] > target) {
+    float acc = s.excl[t];
+    for (int i = i0; i < i1; ++i) {
+      acc += w(i);
+      if (acc > target) {
+        hit = i;
+        break;
+      }
+    }
+  }
+  hit = block_min_int(hit, s.ired);
+  if (hit != INT_MAX) return hit;
+  const int lp = block_max_int(last_pos, s.ired);
+  return lp >= 0 ? lp : 0;
+}
+
+// ------------------------------------------------------------------ top-k candidates
+struct TopKParams {
+  const uint16_t* logits;
+  int64_t stride;
+  int32_t vocab, k;
+  int64_t vocab_start;
+  uint16_t* values;  // [rows, k] bf16
+  int64_t* ids;      // [rows, k]
+};
+
+__global__ __launch_bounds__(kThreads) void topk_candidates_kernel(TopKParams p) {
+  __shared__ uint32_t hist[kSubHists][256];
+  __shared__ uint32_t bins[256];
+  __shared__ uint64_t cand[kMaxTopK];
+  __shared__ int32_t sel[4];  // threshold key, count above, ties needed, candidates written
+  __shared__ int32_t tie_scan[kThreads];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int sub = (t >> 6) * 16 + (lane & 15);
+  const uint16_t* row = p.logits + int64_t(blockIdx.x) * p.stride;
+  const int V = p.vocab;
+  const int kk = min(p.k, V);
+
+  // pass 1: high byte
+  for (int i = t; i < kSubHists * 256; i += kThreads) (&hist[0][0])[i] = 0;
+  __syncthreads();
+  for (int i = t; i < V; i += kThreads) atomicAdd(&hist[sub][bf16_key(row[i]) >> 8], 1u);
+  __syncthreads();
+  {
+    uint32_t c = 0;
+    for (int h = 0; h < kSubHists; ++h) c += hist[h][t];
+    bins[t] = c;
+  }
+  __syncthreads();
+  if (t == 0) {
+    uint32_t above = 0;
+    int hb = 255;
+    for (; hb > 0; --hb) {
+      if (above + bins[hb] >= uint32_t(kk)) break;
+      above += bins[hb];
+    }
+    sel[0] = hb;
+    sel[1] = int(above);
+  }
+  __syncthreads();
+  const uint32_t hb = uint32_t(sel[0]);
+  // pass 2: low byte among keys in the boundary bin
+  for (int i = t; i < kSubHists * 256; i += kThreads) (&hist[0][0])[i] = 0;
+  __syncthreads();
+  for (int i = t; i < V; i += kThreads) {
+    const uint32_t key = bf16_key(row[i]);
+    if ((key >> 8) == hb) atomicAdd(&hist[sub][key & 255], 1u);
+  }
+  __syncthreads();
+  {
+    uint32_t c = 0;
+    for (int h = 0; h < kSubHists; ++h) c += hist[h][t];
+    bins[t] = c;
+  }
+  __syncthreads();
+  if (t == 0) {
+    uint32_t above = uint32_t(sel[1]);
+    int lb = 255;
+    for (; lb > 0; --lb) {
+      if (above + bins[lb] >= uint32_t(kk)) break;
+      above += bins[lb];
+    }
+    sel[0] = int((hb << 8) | uint32_t(lb));  // the k-th largest key
+    sel[1] = int(above);                      // keys above it
+    sel[2] = kk - int(above);                 // ties to take, lowest ids first
+    sel[3] = 0;
+  }
+  __syncthreads();
+  const uint32_t kth = uint32_t(sel[0]);
+  const int ties = sel[2];
+  // pass 3: contiguous chunk per thread so tie ranks follow the id order
+  const int chunk = (V + kThreads - 1) / kThreads;
+  const int i0 = min(t * chunk, V), i1 = min(i0 + chunk, V);
+  int my_ties = 0;
+  for (int i = i0; i < i1; ++i) my_ties += bf16_key(row[i]) == kth;
+  tie_scan[t] = my_ties;
+  __syncthreads();
+  if (t == 0) {
+    int acc = 0;
+    for (int j = 0; j < kThreads; ++j) {
+      const int c = tie_scan[j];
+      tie_scan[j] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  int tie_rank = tie_scan[t];
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t key = bf16_key(row[i]);
+    bool take = key > kth;
+    if (key == kth) take = tie_rank++ < ties;
+    if (take) {
+      const int slot = atomicAdd(&sel[3], 1);
+      // sort key: larger key first, then the lower id
+      cand[slot] = (uint64_t(key) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+    }
+  }
+  __syncthreads();
+  int n2 = 1;
+  while (n2 < kk) n2 <<= 1;
+  for (int i = kk + t; i < n2; i += kThreads) cand[i] = 0;
+  __syncthreads();
+  // bitonic sort, descending
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = t; i < n2; i += kThreads) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool desc = (i & size) == 0;
+          const uint64_t a = cand[i], b = cand[j];
+          if (desc ? a < b : a > b) {
+            cand[i] = b;
+            cand[j] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  uint16_t* vout = p.values + int64_t(blockIdx.x) * p.k;
+  int64_t* iout = p.ids + int64_t(blockIdx.x) * p.k;
+  for (int j = t; j < p.k; j += kThreads) {
+    if (j < kk) {
+      const uint32_t id = 0xffffffffu - uint32_t(cand[j] & 0xffffffffu);
+      vout[j] = row[id];  // the logit's own bits (a -0 stays -0)
+      iout[j] = int64_t(id) + p.vocab_start;
+    } else {
+      vout[j] = 0xff80u;  // -inf, id 0: the reference's padding of a narrow shard
+      iout[j] = 0;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ logits pipe
+struct PipeParams {
+  const void* values;
+  int32_t values_f32;
+  int64_t stride;
+  int32_t width;
+  float inv_temperature;  // 1 when no temperature
+  float top_p;            // >= 1: no top-p
+  float* probs;
+  int64_t out_stride;
+};
+
+__global__ __launch_bounds__(kThreads) void logits_pipe_kernel(PipeParams p) {
+  __shared__ float prob[kMaxPipeWidth];
+  __shared__ uint32_t srt[kMaxPipeWidth];
+  __shared__ float red[kWaves];
+  __shared__ float part[kThreads];
+  __shared__ float cut_value;
+  const int t = threadIdx.x;
+  const int n = p.width;
+  const int64_t r = blockIdx.x;
+  float mx = -FLT_MAX;
+  for (int i = t; i < n; i += kThreads) {
+    float x = p.values_f32 ? static_cast<const float*>(p.values)[r * p.stride + i]
+                           : __uint_as_float(uint32_t(static_cast<const uint16_t*>(p.values)[r * p.stride + i]) << 16);
+    x *= p.inv_temperature;
+    prob[i] = x;
+    mx = fmaxf(mx, x);
+  }
+  mx = block_max(mx, red);
+  float sum = 0.f;
+  for (int i = t; i < n; i += kThreads) {
+    const float e = mx == -INFINITY ? 0.f : expf(prob[i] - mx);
+    prob[i] = e;
+    sum += e;
+  }
+  sum = block_sum(sum, red);
+  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+  for (int i = t; i < n; i += kThreads) prob[i] *= inv;
+  __syncthreads();
+  float* out = p.probs + r * p.out_stride;
+  if (!(p.top_p < 1.f)) {
+    for (int i = t; i < n; i += kThreads) out[i] = prob[i];
+    return;
+  }
+  // sort the probabilities (non-negative: float bits order like integers), descending
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (int i = t; i < n2; i += kThreads) srt[i] = i < n ? __float_as_uint(prob[i]) : 0u;
+  __syncthreads();
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = t; i < n2; i += kThreads) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool desc = (i & size) == 0;
+          const uint32_t a = srt[i], b = srt[j];
+          if (desc ? a < b : a > b) {
+            srt[i] = b;
+            srt[j] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // prefix sums of the sorted values: a contiguous chunk per thread, chunk sums in thread order
+  const int chunk = (n + kThreads - 1) / kThreads;
+  const int i0 = min(t * chunk, n), i1 = min(i0 + chunk, n);
+  float s = 0.f;
+  for (int i = i0; i < i1; ++i) s += __uint_as_float(srt[i]);
+  part[t] = s;
+  __syncthreads();
+  if (t == 0) {
+    float acc = 0.f;
+    for (int j = 0; j < kThreads; ++j) {
+      const float c = part[j];
+      part[j] = acc;
+      acc += c;
+    }
+    cut_value = __uint_as_float(srt[n - 1]);  // no prefix reaches top_p: keep everything
+  }
+  __syncthreads();
+  // the smallest prefix reaching top_p ends in exactly one thread's chunk
+  {
+    float acc = part[t];
+    const float before = acc;
+    for (int i = i0; i < i1; ++i) {
+      const float prev = acc;
+      acc += __uint_as_float(srt[i]);
+      if (acc >= p.top_p && (i == i0 ? before < p.top_p : prev < p.top_p)) cut_value = __uint_as_float(srt[i]);
+    }
+  }
+  __syncthreads();
+  const float thresh = cut_value;
+  float kept = 0.f;
+  for (int i = t; i < n; i += kThreads) kept += prob[i] >= thresh ? prob[i] : 0.f;
+  kept = block_sum(kept, red);
+  const float rk = kept > 0.f ? 1.f / kept : 0.f;
+  for (int i = t; i < n; i += kThreads) out[i] = prob[i] >= thresh ? prob[i] * rk : 0.f;
+}
+
+// ------------------------------------------------------------------ draws
+__global__ __launch_bounds__(kThreads) void sample_kernel(const float* probs, int64_t stride, int32_t vocab,
+                                                          const float* uniforms, int32_t* out) {
+  __shared__ DrawLds s;
+  const float* row = probs + int64_t(blockIdx.x) * stride;
+  const int idx = block_draw([&](int i) { return row[i]; }, vocab, uniforms[blockIdx.x], s);
+  if (threadIdx.x == 0) out[blockIdx.x] = idx;
+}
+
+struct ChainParams {
+  const float* draft_probs;      // [R, D, V]
+  const int32_t* draft_ids;      // [R, D]
+  const float* target_probs;     // [R, D + 1, V]
+  const float* uniforms;         // [R, D + 1]
+  int32_t num_spec, vocab;
+  int32_t* output;               // [R, D + 1]
+  int32_t* accepted;             // [R] or null
+  int32_t* emitted;              // [R]
+};
+
+__global__ __launch_bounds__(kThreads) void chain_kernel(ChainParams p) {
+  __shared__ DrawLds s;
+  __shared__ int stop;
+  const int64_t r = blockIdx.x;
+  const int D = p.num_spec, V = p.vocab;
+  const float* q = p.draft_probs + r * D * V;
+  const float* pt = p.target_probs + r * (D + 1) * V;
+  const float* u = p.uniforms + r * (D + 1);
+  const int32_t* x = p.draft_ids + r * D;
+  if (threadIdx.x == 0) {
+    int j = D, acc = 0;
+    for (int i = 0; i < D; ++i) {
+      const int xi = min(max(x[i], 0), V - 1);
+      const bool ok = u[i] * q[int64_t(i) * V + xi] < pt[int64_t(i) * V + xi];
+      acc += ok;
+      if (!ok && j == D) j = i;
+    }
+    stop = j;
+    if (p.accepted) p.accepted[r] = acc;
+    p.emitted[r] = j;
+  }
+  __syncthreads();
+  const int j = stop;
+  const float* pj = pt + int64_t(j) * V;
+  const float* qj = q + int64_t(min(j, D - 1)) * V;
+  float wsum = 0.f;
+  for (int i = threadIdx.x; i < V; i += kThreads) wsum += j < D ? fmaxf(pj[i] - qj[i], 0.f) : pj[i];
+  wsum = block_sum(wsum, s.fred);
+  const bool residual = j < D && wsum > 0.f;
+  const int tok = block_draw([&](int i) { return residual ? fmaxf(pj[i] - qj[i], 0.f) : pj[i]; }, V, u[D], s);
+  int32_t* out = p.output + r * (D + 1);
+  for (int i = threadIdx.x; i <= D; i += kThreads) out[i] = i < j ? x[i] : (i == j ? tok : -1);
+}
+
+// The reference's top-k verification (aspire/engine/sampling.py:46-98) in one launch: the
+// chain rule over a local vocabulary of top_k + 1 entries built on the fly. Local entry
+// v < K of position i is the target's candidate v; entry K stands for "a token outside the
+// target's top-k". Draft probabilities map onto the target's candidates by id (ids are unique
+// within a row, so each entry takes at most one term).
+struct VerifyParams {
+  const float* draft_probs;    // [R, D, K]
+  const int64_t* draft_ids;    // [R, D, K]
+  const int32_t* draft_tokens; // [R, D]
+  const int32_t* draft_counts; // [R]
+  const float* target_probs;   // [R, D + 1, K]
+  const int64_t* target_ids;   // [R, D + 1, K]
+  const float* uniforms;       // [R, D + 1]
+  int32_t num_spec, top_k;
+  int64_t* output;             // [R, D + 1]
+  int32_t* emitted;            // [R]
+};
+
+__global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
+  __shared__ DrawLds s;
+  __shared__ int local_tok[64];
+  __shared__ float qx[64];
+  __shared__ int stop;
+  const int64_t r = blockIdx.x;
+  const int D = p.num_spec, K = p.top_k;
+  const int n = p.draft_counts[r];
+  const float* dp = p.draft_probs + r * D * K;
+  const int64_t* di = p.draft_ids + r * D * K;
+  const float* tp = p.target_probs + r * (D + 1) * K;
+  const int64_t* ti = p.target_ids + r * (D + 1) * K;
+  const float* u = p.uniforms + r * (D + 1);
+  // wave i handles position i: local token and its local draft probability
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int i = wave; i < D; i += kWaves) {
+    const int64_t tok = p.draft_tokens[r * D + i];
+    int first = INT_MAX;
+    for (int v = lane; v < K; v += 64)
+      if (ti[int64_t(i) * K + v] == tok) first = min(first, v);
+    first = wave_min_int(first);
+    const bool valid = i < n;
+    const int lt = (valid && first != INT_MAX) ? first : K;
+    // draft probability of the local token's id (the target's candidate, or the draft token)
+    const int64_t want = lt < K ? ti[int64_t(i) * K + lt] : tok;
+    float qsum = 0.f;
+    for (int m = lane; m < K; m += 64) qsum += di[int64_t(i) * K + m] == want ? dp[int64_t(i) * K + m] : 0.f;
+    qsum = wave_sum(qsum);
+    if (lane == 0) {
+      local_tok[i] = lt;
+      qx[i] = valid ? qsum : 1.f;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int j = D;
+    for (int i = 0; i < D; ++i) {
+      const int lt = local_tok[i];
+      const float pv = (lt < K && i <= n) ? tp[int64_t(i) * K + lt] : 0.f;
+      if (!(u[i] * qx[i] < pv)) {
+        j = i;
+        break;
+      }
+    }
+    stop = j;
+  }
+  __syncthreads();
+  const int j = stop;
+  // local distributions at position j: target P (masked past the draft count), draft Q
+  const bool pj_ok = j <= n;
+  auto P = [&](int v) { return (v < K && pj_ok) ? tp[int64_t(j) * K + v] : 0.f; };
+  auto Q = [&](int v) -> float {
+    if (v >= K || j >= n) return 0.f;  // entry K only ever lowers max(P - Q, 0), which is 0 there
+    const int64_t id = ti[int64_t(j) * K + v];
+    float q = 0.f;
+    for (int m = 0; m < K; ++m) q += di[int64_t(j) * K + m] == id ? dp[int64_t(j) * K + m] : 0.f;
+    return q;
+  };
+  float wsum = 0.f;
+  if (j < D)
+    for (int v = threadIdx.x; v <= K; v += kThreads) wsum += fmaxf(P(v) - Q(v), 0.f);
+  wsum = block_sum(wsum, s.fred);
+  const bool residual = j < D && wsum > 0.f;
+  const int lt = block_draw([&](int v) { return residual ? fmaxf(P(v) - Q(v), 0.f) : P(v); }, K + 1, u[D], s);
+  const int emitted = min(j, n);
+  int64_t* out = p.output + r * (D + 1);
+  for (int i = threadIdx.x; i <= D; i += kThreads) {
+    const int l = i < j ? local_tok[i] : (i == j ? lt : -1);
+    out[i] = (l >= 0 && l < K && i <= emitted) ? ti[int64_t(i) * K + l] : -1;
+  }
+  if (threadIdx.x == 0) p.emitted[r] = emitted;
+}
+
+}  // namespace
+}  // namespace aspire
+
+extern "C" int aspire_topk_candidates(const void* logits, int64_t stride, int32_t rows, int32_t vocab, int32_t top_k,
+                                      int64_t vocab_start, void* values, int64_t* ids, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(rows >= 0 && vocab >= 1 && top_k >= 1 && top_k <= kMaxTopK, "need vocab >= 1, 1 <= top_k <= 1024");
+  ASPIRE_CHECK_ARG(vocab <= (1 << 30) && stride >= vocab, "bad vocab / row stride");
+  if (rows == 0) return ASPIRE_OK;
+  ASPIRE_CHECK_ARG(logits && values && ids, "null pointer");
+  TopKParams p{static_cast<const uint16_t*>(logits), stride, vocab, top_k, vocab_start,
+               static_cast<uint16_t*>(values), ids};
+  hipLaunchKernelGGL(topk_candidates_kernel, dim3(rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+  ASPIRE_CHECK_LAUNCH();
+  return ASPIRE_OK;
+}
+
+extern "C" int aspire_logits_pipe(const void* values, int32_t values_dtype, int64_t stride, int32_t rows, int32_t width,
+                                  float temperature, float top_p, float* probs, int64_t out_stride, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(rows >= 0 && width >= 1 && width <= kMaxPipeWidth, "width must be in [1, 4096]");
+  ASPIRE_CHECK_ARG(values_dtype == 0 || values_dtype == 1, "values_dtype must be 0 (bf16) or 1 (fp32)");
+  ASPIRE_CHECK_ARG(stride >= width && out_stride >= width, "bad row strides");
+  if (rows == 0) return ASPIRE_OK;
+  ASPIRE_CHECK_ARG(values && probs, "null pointer");
+  PipeParams p{values, values_dtype, stride, width, temperature > 0.f ? 1.f / temperature : 1.f,
+               (top_p > 0.f && top_p < 1.f) ? top_p : 2.f, probs, out_stride};
+  hipLaunchKernelGGL(logits_pipe_kernel, dim3(rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+  ASPIRE_CHECK_LAUNCH();
+  return ASPIRE_OK;
+}
+
+extern "C" int aspire_sampling_from_probs(const float* probs, int64_t stride, int32_t rows, int32_t vocab,
+                                          const float* uniforms, int32_t* out, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(rows >= 0 && vocab >= 1 && stride >= vocab, "bad vocab / row stride");
+  if (rows == 0) return ASPIRE_OK;
+  ASPIRE_CHECK_ARG(probs && uniforms && out, "null pointer");
+  hipLaunchKernelGGL(sample_kernel, dim3(rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream), probs, stride,
+                     vocab, uniforms, out);
+  ASPIRE_CHECK_LAUNCH();
+  return ASPIRE_OK;
+}
+
+extern "C" int aspire_chain_speculative_sampling(const float* draft_probs, const int32_t* draft_token_ids,
+                                                 const float* target_probs, int32_t rows, int32_t num_spec,
+                                                 int32_t vocab, const float* uniforms, int32_t* output_token_ids,
+                                                 int32_t* accepted_num, int32_t* emitted_num, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(rows >= 0 && num_spec >= 1 && vocab >= 1, "need num_spec >= 1 and vocab >= 1");
+  if (rows == 0) return ASPIRE_OK;
+  ASPIRE_CHECK_ARG(draft_probs && draft_token_ids && target_probs && uniforms && output_token_ids && emitted_num,
+                   "null pointer");
+  ChainParams p{draft_probs, draft_token_ids, target_probs, uniforms, num_spec, vocab, output_token_ids, accepted_num,
+                emitted_num};
+  hipLaunchKernelGGL(chain_kernel, dim3(rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+  ASPIRE_CHECK_LAUNCH();
+  return ASPIRE_OK;
+}
+
+extern "C" int aspire_verify_topk_speculation(const float* draft_probs, const int64_t* draft_ids,
+                                              const int32_t* draft_tokens, const int32_t* draft_counts,
+                                              const float* target_probs, const int64_t* target_ids,
+                                              const float* uniforms, int32_t requests, int32_t max_draft,
+                                              int32_t top_k, int64_t* output, int32_t* emitted, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(requests >= 0 && max_draft >= 1 && max_draft <= 64 && top_k >= 1,
+                   "need 1 <= max_draft <= 64 and top_k >= 1");
+  if (requests == 0) return ASPIRE_OK;
+  ASPIRE_CHECK_ARG(draft_probs && draft_ids && draft_tokens && draft_counts && target_probs && target_ids &&
+                       uniforms && output && emitted,
+                   "null pointer");
+  VerifyParams p{draft_probs, draft_ids, draft_tokens, draft_counts, target_probs, target_ids, uniforms,
+                 max_draft, top_k, output, emitted};
+  hipLaunchKernelGGL(verify_kernel, dim3(requests), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+  ASPIRE_CHECK_LAUNCH();
+  return ASPIRE_OK;
+}

@@ -484,6 +484,40 @@ def measure_components(step, w, out, steps, plan_us):
     res["merge"] = entry(us, merge_bytes, merges=info.num_merge, partial_rows=info.partial_rows,
                          note="20 calls per graph replay; bytes = fp32 partials read + 16 bf16 rows out per merge")
 
+    # (f4) sampling at the config-3 decode step's size: 208 tokens' top-50 candidates over the
+    # 151,936-entry vocabulary, the temperature/softmax/top-p pipe, one draw per token, and the
+    # speculative verification of 32 requests x 8 drafts over their top-50 candidates
+    from aspire_amd.engine.sampling import local_topk_candidates, verify_topk_speculation
+    from aspire_amd.logits_processor import build_logits_pipe
+    from aspire_amd.sampling import sampling_from_probs
+    gs = torch.Generator(device=dev).manual_seed(11)
+    logits = torch.randn(208, 151936, generator=gs, device=dev).to(torch.bfloat16)
+    pipe, pkw = build_logits_pipe(0.8, 0.9)
+    u = torch.rand(208, generator=gs, device=dev)
+
+    def sample_step():
+        vals, ids = local_topk_candidates(logits, 50)
+        sampling_from_probs(pipe(vals, **pkw), uniforms=u)
+
+    us_s = graph_timed(sample_step, steps, stream) * 1e3
+    R, D, K = 32, 8, 50
+    tprobs = torch.softmax(torch.randn(R, D + 1, K, generator=gs, device=dev), -1)
+    dprobs = torch.softmax(torch.randn(R, D, K, generator=gs, device=dev), -1)
+    tids = torch.randint(0, 151936, (R, D + 1, K), generator=gs, device=dev)
+    dids = tids[:, :D].clone()
+    dtok = dids[:, :, 0].to(torch.int32)
+    dcnt = torch.full((R,), D, dtype=torch.int32, device=dev)
+    uv = torch.rand(R, D + 1, generator=gs, device=dev)
+    us_v = graph_timed(lambda: verify_topk_speculation(dprobs, dids, dtok, dcnt, tprobs, tids, uniforms=uv),
+                       steps, stream) * 1e3
+    res["sampling"] = {"topk_pipe_draw_us": round(us_s, 2), "rows": 208, "vocab": 151936, "top_k": 50,
+                       "logits_bytes": 208 * 151936 * 2,
+                       "logits_gbs": _gbs(208 * 151936 * 2, us_s),
+                       "verify_us": round(us_v, 2), "verify_requests": R, "verify_drafts": D,
+                       "note": "20 calls per graph replay; top-k candidates + LogitsPipe(temperature 0.8, "
+                               "top-p 0.9) + sampling_from_probs; verify_topk_speculation in one launch"}
+    del logits
+
     # (f3) chunked prefill: one 8192-token prompt chunk (the reference's max_prefill_tokens) over an empty
     # prefix, and 4 x 2048-token chunks over 6144 cached tokens each, Qwen3-8B heads; causal
     from aspire_amd.attention.prefill import BatchPrefillWithPagedKVCacheWrapper

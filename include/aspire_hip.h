@@ -438,6 +438,59 @@ int aspire_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int6
 int aspire_argmax_rows(const void* logits, int64_t stride, int32_t rows, int32_t vocab, int64_t* ids,
                        void* stream);
 
+/* ------------------------------------------------------ (f4) sampling
+ * Token sampling and speculative verification. One workgroup per row or request; the
+ * uniforms of every draw are explicit device inputs (the Python layer draws them with
+ * torch's generator, so a run is reproducible and graph-capturable). */
+
+/* local_topk_candidates (aspire/engine/sampling.py:6-29) on one rank: the top_k
+ * (1..1024) largest bf16 logits of each row, descending (ties: lower id first), into
+ * values [rows, top_k] bf16 and ids [rows, top_k] (+ vocab_start); rows narrower than
+ * top_k are padded with -inf / id 0 as the reference pads a narrow vocabulary shard. */
+int aspire_topk_candidates(const void* logits, int64_t stride, int32_t rows, int32_t vocab, int32_t top_k,
+                           int64_t vocab_start, void* values, int64_t* ids, void* stream);
+
+/* LogitsPipe([Temperature(), Softmax(), TopP()]) behind mylib::logit_process
+ * (aspire/models/sparse_draft_runner.py:527-554): per row of width (<= 4096) values
+ * (values_dtype 0 bf16, 1 fp32), probs = softmax(values / temperature) in fp32 (no
+ * temperature when <= 0), then top-p renormalisation when 0 < top_p < 1: the smallest
+ * set of the largest probabilities whose sum reaches top_p (every probability equal to
+ * its smallest member included) is kept and divided by its sum, the rest set to 0. */
+int aspire_logits_pipe(const void* values, int32_t values_dtype, int64_t stride, int32_t rows, int32_t width,
+                       float temperature, float top_p, float* probs, int64_t out_stride, void* stream);
+
+/* FlashInfer sampling_from_probs (called at aspire/engine/runtime.py:709,748): out[r] =
+ * the first index whose inclusive prefix sum of probs[r] exceeds uniforms[r] * sum
+ * (uniforms in [0, 1)); the last positive index if rounding leaves none. */
+int aspire_sampling_from_probs(const float* probs, int64_t stride, int32_t rows, int32_t vocab,
+                               const float* uniforms, int32_t* out, void* stream);
+
+/* FlashInfer chain_speculative_sampling (called at aspire/engine/sampling.py:84-86):
+ * draft_probs [rows, num_spec, vocab], draft_token_ids [rows, num_spec], target_probs
+ * [rows, num_spec + 1, vocab], uniforms [rows, num_spec + 1], all contiguous. Draft i
+ * is accepted while uniforms[r, i] * q_i(x_i) < p_i(x_i); at the first rejection j a
+ * token is drawn (with uniforms[r, num_spec]) from max(0, p_j - q_j) normalised (from
+ * p_j if that is all zero), after a full acceptance from p_{num_spec}.
+ * output_token_ids [rows, num_spec + 1]: accepted drafts, the drawn token, then -1;
+ * emitted_num[r] = j; accepted_num[r] (optional) = the positions that pass the test on
+ * their own, chain or not. */
+int aspire_chain_speculative_sampling(const float* draft_probs, const int32_t* draft_token_ids,
+                                      const float* target_probs, int32_t rows, int32_t num_spec, int32_t vocab,
+                                      const float* uniforms, int32_t* output_token_ids, int32_t* accepted_num,
+                                      int32_t* emitted_num, void* stream);
+
+/* verify_topk_speculation (aspire/engine/sampling.py:46-98) in one launch: the chain
+ * rule over each position's local vocabulary of the target's top_k candidates plus one
+ * entry for tokens outside them. draft_probs / draft_ids [requests, max_draft, top_k],
+ * draft_tokens [requests, max_draft] int32, draft_counts [requests] int32, target_probs /
+ * target_ids [requests, max_draft + 1, top_k], uniforms [requests, max_draft + 1];
+ * output [requests, max_draft + 1] int64 (vocabulary ids, -1 past the emitted tokens),
+ * emitted [requests] int32 (accepted drafts). max_draft <= 64. */
+int aspire_verify_topk_speculation(const float* draft_probs, const int64_t* draft_ids, const int32_t* draft_tokens,
+                                   const int32_t* draft_counts, const float* target_probs, const int64_t* target_ids,
+                                   const float* uniforms, int32_t requests, int32_t max_draft, int32_t top_k,
+                                   int64_t* output, int32_t* emitted, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,218 @@
+"""Sampling and speculative verification kernels on the GPU against the CPU oracle, with the
+same uniforms. Integer outputs must match exactly wherever the decision is not within float
+rounding of a boundary (such draws are counted and must be rare); probabilities match within
+fp32 rounding. A frequency test checks the GPU chain keeps the target distribution on its own."""
+
+import numpy as np
+import pytest
+import torch
+
+from aspire_amd.engine.sampling import local_topk_candidates, merge_topk_candidates, verify_topk_speculation
+from aspire_amd.logits_processor import build_logits_pipe, define_logit_process_op
+from aspire_amd.sampling import chain_speculative_sampling, sampling_from_probs
+from helpers import say
+from oracle import sampling as osamp
+
+pytestmark = pytest.mark.gpu
+
+MARGIN = 1e-5
+
+
+@pytest.mark.parametrize("rows,vocab,k,start", [(208, 151936, 50, 0), (33, 1000, 64, 7), (5, 37, 50, 151936),
+                                                 (4, 4096, 1024, 0)])
+def test_topk_candidates_exact(gpu, rows, vocab, k, start):
+    say("topk candidates", rows, vocab, k)
+    g = torch.Generator().manual_seed(vocab + k)
+    # coarse logits: many equal bf16 values, so the tie rule decides the boundary
+    logits = (torch.randn(rows, vocab, generator=g) * 3).round().to(torch.bfloat16)
+    logits[0, :5] = float("inf")                                  # +inf sorts above every finite logit
+    vals, ids = local_topk_candidates(logits.to(gpu), k, vocab_start=start)
+    torch.cuda.synchronize()
+    ref_v, ref_i = osamp.topk_candidates(logits, k, vocab_start=start)
+    assert torch.equal(ids.cpu(), ref_i)
+    assert torch.equal(vals.cpu().view(torch.int16), ref_v.view(torch.int16))
+
+
+def test_merge_topk_candidates(gpu):
+    g = torch.Generator().manual_seed(3)
+    vals = (torch.randn(6, 4 * 50, generator=g) * 2).round().to(torch.bfloat16)
+    ids = torch.randint(0, 151936, (6, 200), generator=g)
+    mv, mi = merge_topk_candidates(vals.to(gpu), ids.to(gpu), 50)
+    rv, ri = osamp.topk_candidates(vals, 50)
+    assert torch.equal(mv.cpu().view(torch.int16), rv.view(torch.int16))
+    assert torch.equal(mi.cpu(), torch.gather(ids, 1, ri))
+
+
+@pytest.mark.parametrize("temperature,top_p,dtype", [(0.7, 0.9, torch.bfloat16), (1.0, 0.5, torch.float32),
+                                                     (1.3, 0.0, torch.bfloat16), (0.0, 0.95, torch.float32)])
+def test_logits_pipe_matches_oracle(gpu, temperature, top_p, dtype):
+    say("logits pipe", temperature, top_p, dtype)
+    g = torch.Generator().manual_seed(int(temperature * 10 + top_p * 100))
+    vals = (torch.randn(64, 50, generator=g) * 2).to(dtype)
+    vals[3, 10:] = float("-inf")                                  # a padded narrow shard
+    pipe, kw = build_logits_pipe(temperature, top_p)
+    probs = pipe(vals.to(gpu), **kw)
+    torch.cuda.synchronize()
+    ref = osamp.logits_pipe(vals.float(), temperature=temperature if temperature > 0 else None,
+                            top_p=top_p if top_p > 0 else None)
+    got = probs.cpu()
+    skipped = 0
+    for r in range(64):
+        if top_p > 0:
+            base = osamp.logits_pipe(vals[r : r + 1].float(), temperature=temperature if temperature > 0 else None)
+            if osamp.cut_margin(base[0].numpy(), top_p) < MARGIN:
+                skipped += 1
+                continue
+            assert torch.equal(got[r] > 0, ref[r] > 0), r                # the same kept set
+        assert torch.allclose(got[r], ref[r], rtol=1e-5, atol=1e-7), r
+    assert skipped <= 2
+
+
+def test_sampling_from_probs_matches_oracle(gpu):
+    say("sampling_from_probs")
+    rng = np.random.default_rng(4)
+    R, V = 512, 51
+    p = rng.dirichlet(np.full(V, 0.3), size=R).astype(np.float32)
+    p[::7, 20:] = 0                                                  # zero tails
+    u = rng.random(R).astype(np.float32)
+    u[0] = 0.0
+    got = sampling_from_probs(torch.from_numpy(p).to(gpu), uniforms=torch.from_numpy(u).to(gpu)).cpu()
+    ref = osamp.sample_from_probs(torch.from_numpy(p), torch.from_numpy(u))
+    amb = [r for r in range(R) if osamp.draw_margin(p[r], float(u[r])) < MARGIN]
+    ok = [r for r in range(R) if r not in amb]
+    assert got.dtype == torch.int32 and len(amb) <= 3
+    assert torch.equal(got[ok].long(), ref[ok])
+    # a wide row (the whole vocabulary) through the chunked scan
+    big = rng.random((4, 151936)).astype(np.float32) ** 8
+    ub = rng.random(4).astype(np.float32)
+    gb = sampling_from_probs(torch.from_numpy(big).to(gpu), uniforms=torch.from_numpy(ub).to(gpu)).cpu()
+    rb = osamp.sample_from_probs(torch.from_numpy(big), torch.from_numpy(ub))
+    for r in range(4):
+        if osamp.draw_margin(big[r], float(ub[r])) >= MARGIN:
+            assert gb[r].item() == rb[r].item()
+
+
+def _chain_inputs(rng, R, D, V, agree=0.6):
+    target = rng.dirichlet(np.full(V, 0.5), size=(R, D + 1)).astype(np.float32)
+    noise = rng.dirichlet(np.full(V, 0.5), size=(R, D)).astype(np.float32)
+    draft = (agree * target[:, :D] + (1 - agree) * noise).astype(np.float32)
+    x = np.stack([[rng.choice(V, p=draft[r, i] / draft[r, i].sum()) for i in range(D)] for r in range(R)])
+    return draft, x.astype(np.int32), target
+
+
+def test_chain_speculative_sampling_matches_oracle(gpu):
+    say("chain speculative sampling")
+    rng = np.random.default_rng(5)
+    R, D, V = 256, 5, 51
+    draft, x, target = _chain_inputs(rng, R, D, V)
+    u = rng.random((R, D + 1)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(gpu)
+    acc_in = torch.full((R,), 3, dtype=torch.int32, device=gpu)
+    out, acc, em = chain_speculative_sampling(t(draft), t(x), t(target), maybe_output_accepted_token_num=acc_in,
+                                              uniforms=t(u))
+    torch.cuda.synchronize()
+    ref_out, ref_acc, ref_em = osamp.chain_speculative_sampling(torch.from_numpy(draft), torch.from_numpy(x),
+                                                                torch.from_numpy(target), torch.from_numpy(u))
+    amb = [r for r in range(R) if osamp.chain_draw_margin(torch.from_numpy(draft), torch.from_numpy(x),
+                                                          torch.from_numpy(target), torch.from_numpy(u), r) < MARGIN]
+    ok = [r for r in range(R) if r not in amb]
+    assert len(amb) <= 3
+    assert torch.equal(out.cpu()[ok], ref_out[ok])
+    assert torch.equal(em.cpu()[ok], ref_em[ok])
+    assert torch.equal(acc.cpu()[ok], ref_acc[ok] + 3)            # added in place
+    assert acc is acc_in and 0 < int(ref_em.sum()) < R * D         # a mix of accepts and rejects
+
+
+def test_chain_keeps_the_target_distribution_on_gpu(gpu):
+    """Frequency check of the GPU kernel alone: the first emitted token follows p_0 for any q_0."""
+    say("chain frequency")
+    rng = np.random.default_rng(6)
+    V, n = 6, 200000
+    q0 = np.array([0.4, 0.3, 0.1, 0.1, 0.05, 0.05])
+    p0 = np.array([0.05, 0.1, 0.15, 0.2, 0.2, 0.3])
+    x = torch.from_numpy(rng.choice(V, size=(n, 1), p=q0).astype(np.int32)).to(gpu)
+    dp = torch.from_numpy(q0.astype(np.float32)).to(gpu).expand(n, 1, V).contiguous()
+    tp = torch.from_numpy(np.stack([p0, p0]).astype(np.float32)).to(gpu).expand(n, 2, V).contiguous()
+    out, _, _ = chain_speculative_sampling(dp, x, tp, generator=torch.Generator(device=gpu).manual_seed(1))
+    counts = np.bincount(out[:, 0].cpu().numpy(), minlength=V)
+    exp = p0 * n
+    stat = float(((counts - exp) ** 2 / exp).sum())
+    assert stat < 20.52, stat                                      # chi-square 0.999 quantile, 5 dof
+
+
+def test_verify_topk_speculation_matches_oracle(gpu):
+    say("verify_topk_speculation")
+    rng = np.random.default_rng(7)
+    R, D, K, vocab = 64, 6, 50, 151936
+    target_ids = np.stack([rng.choice(vocab, size=K, replace=False) for _ in range(R * (D + 1))]).reshape(R, D + 1, K)
+    # draft candidates: mostly the target's, some replaced by other ids, in another order
+    draft_ids = target_ids[:, :D].copy()
+    for r in range(R):
+        for i in range(D):
+            draft_ids[r, i] = rng.permutation(draft_ids[r, i])
+            swap = rng.random(K) < 0.2
+            draft_ids[r, i, swap] = rng.choice(vocab, size=int(swap.sum()), replace=False) + vocab
+    target_probs = rng.dirichlet(np.full(K, 0.4), size=(R, D + 1)).astype(np.float32)
+    draft_probs = rng.dirichlet(np.full(K, 0.4), size=(R, D)).astype(np.float32)
+    tok = np.stack([[draft_ids[r, i, rng.choice(K, p=draft_probs[r, i])] for i in range(D)] for r in range(R)])
+    counts = rng.integers(0, D + 1, size=R).astype(np.int32)
+    u = rng.random((R, D + 1)).astype(np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    out, emitted = verify_topk_speculation(T(draft_probs).to(gpu), T(draft_ids).to(gpu), T(tok.astype(np.int32)).to(gpu),
+                                           T(counts).to(gpu), T(target_probs).to(gpu), T(target_ids).to(gpu),
+                                           uniforms=T(u).to(gpu))
+    torch.cuda.synchronize()
+    ref_out, ref_em, (ld, lt, ltg) = osamp.verify_topk_speculation(T(draft_probs), T(draft_ids), T(tok.astype(np.int32)),
+                                                                   T(counts), T(target_probs), T(target_ids), T(u))
+    amb = [r for r in range(R) if osamp.chain_draw_margin(ld, lt, ltg, T(u), r) < MARGIN]
+    ok = [r for r in range(R) if r not in amb]
+    assert len(amb) <= 2
+    assert out.dtype == torch.int64 and emitted.dtype == torch.int32
+    assert torch.equal(out.cpu()[ok], ref_out[ok])
+    assert torch.equal(emitted.cpu()[ok], ref_em[ok])
+    assert 0 < int(ref_em.sum()) < int(counts.sum())
+
+
+def test_sampling_graph_replays(gpu):
+    """Top-k + pipe + draws captured in a HIP graph with torch.rand uniforms: each replay draws
+    new uniforms, and each replay's tokens equal the oracle's on that replay's uniforms."""
+    say("sampling graph")
+    g = torch.Generator().manual_seed(9)
+    logits = torch.randn(16, 8192, generator=g).to(torch.bfloat16).to(gpu)
+    pipe, kw = build_logits_pipe(0.8, 0.9)
+    u = torch.empty(16, device=gpu)
+    out = torch.empty(16, dtype=torch.int32, device=gpu)
+    probs_buf = torch.empty(16, 50, device=gpu)
+
+    def step():
+        vals, ids = local_topk_candidates(logits, 50)
+        probs_buf.copy_(pipe(vals, **kw))
+        u.copy_(torch.rand(16, device=gpu))
+        out.copy_(sampling_from_probs(probs_buf, uniforms=u))
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    seen = []
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = osamp.sample_from_probs(probs_buf.cpu(), u.cpu())
+        for r in range(16):
+            if osamp.draw_margin(probs_buf[r].cpu().numpy(), float(u[r])) >= MARGIN:
+                assert out[r].item() == ref[r].item(), (rep, r)
+        seen.append(u.cpu().clone())
+        _ = torch.randn(100, device=gpu).sum().item()
+    assert not torch.equal(seen[0], seen[1])
+
+
+def test_logit_process_op(gpu):
+    pipe, kw = build_logits_pipe(0.9, 0.8)
+    op = define_logit_process_op(pipe, kw)
+    vals = torch.randn(8, 50, device=gpu).to(torch.bfloat16)
+    assert torch.equal(op(vals), pipe(vals, **kw))
+    with torch._subclasses.fake_tensor.FakeTensorMode():
+        fake = torch.empty(8, 50, dtype=torch.bfloat16, device=gpu)
+        assert op(fake).dtype == torch.float32
