@@ -416,3 +416,42 @@ def build_holistic_dump_jit_args(
         tensor_types.append("int32_t")
     return [op_name, dtype, dtype, dtype, torch.int32, head_dim, head_dim, tensor_names, tensor_types,
             scalar_names, scalar_types, class_name, spec]
+
+
+def define_unified_decode_op(wrapper: HolisticAttentionWrapper, op_name: str = "mylib::unified_decode"):
+    """Register ``mylib::unified_decode(Tensor q, Tensor kv_cache, Tensor(a!) out) -> ()`` over
+    ``wrapper`` (aspire/models/sparse_draft_runner.py:599-612): the op runs the planned mixed
+    attention into ``out``; its fake implementation returns nothing, so torch.compile traces
+    the call without running it."""
+    torch.library.define(op_name, "(Tensor q, Tensor kv_cache, Tensor(a!) out) -> ()")
+
+    @torch.library.impl(op_name, "cuda")
+    def _unified_decode(q, kv_cache, out):
+        wrapper.run(q, kv_cache, out=out)
+
+    @torch.library.register_fake(op_name)
+    def _unified_decode_fake(q, kv_cache, out):
+        return None
+
+    return getattr(torch.ops.mylib, op_name.split("::", 1)[1])
+
+
+def define_dump_op(wrapper: HolisticAttentionWrapper, op_name: str, num_heads: int, kv_stride: int,
+                   mode_flags: Optional[torch.Tensor] = None):
+    """Register the refresh layer's dump op ``(Tensor q, Tensor kv_cache, Tensor(a!) dump_buffer,
+    Tensor(b!) out) -> Tensor`` over a wrapper built with dump ``jit_args``
+    (aspire/backends/base.py:452-489): it runs the full attention, writes the logits dump and
+    returns the base-2 LSE ``[T, num_heads]`` fp32 (its fake implementation returns an empty one)."""
+    torch.library.define(op_name, "(Tensor q, Tensor kv_cache, Tensor(a!) dump_buffer, Tensor(b!) out) -> Tensor")
+
+    @torch.library.impl(op_name, "cuda")
+    def _dump_kernel(q, kv_cache, dump_buffer, out):
+        args = [q, kv_cache, dump_buffer] + ([mode_flags] if mode_flags is not None else []) + [num_heads, kv_stride]
+        _, lse = wrapper.run(*args, return_lse=True, out=out)
+        return lse
+
+    @torch.library.register_fake(op_name)
+    def _dump_kernel_fake(q, kv_cache, dump_buffer, out):
+        return torch.empty((q.shape[0], num_heads), dtype=torch.float32, device=q.device)
+
+    return getattr(torch.ops.mylib, op_name.split("::", 1)[1])
