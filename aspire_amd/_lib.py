@@ -8,12 +8,15 @@ PyTorch fallback: if the library is missing every entry point raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libaspire_hip.so"
+# ASPIRE_HIP_LIB selects another build of the same library (a compile-time kernel variant made
+# with ``build.py --define ... --out ...``), for A/B measurements.
+LIB_PATH = Path(os.environ.get("ASPIRE_HIP_LIB") or Path(__file__).resolve().parent / "libaspire_hip.so").resolve()
 
 ASPIRE_OK = 0
 ASPIRE_ERR_INVALID = 1

@@ -91,6 +91,14 @@ constexpr float kNegInf = -__builtin_huge_valf();
 #define ASPIRE_STAGED_MAX_NT 2
 #endif
 
+// Items of at most 4 query rows (one token's GQA group of 4, a draft row) on VALU
+// v_dot2 / DPP reductions instead of MFMA. Off by default: see the A/B of the two
+// paths in the counter profiles of the attention kernel.
+#ifndef ASPIRE_DRAFT_VALU
+#define ASPIRE_DRAFT_VALU 0
+#endif
+constexpr int kValuRows = 4;
+
 // Workgroup-staged K/V (1-tile items of head-aligned plans): LDS per workgroup,
 // two buffers x {K, V} x 16 key rows x 1 KiB (the rows' 4 heads), in uint4.
 constexpr int kStageRowChunks = 64;                      // 16-byte chunks per 1 KiB row-half
@@ -150,6 +158,30 @@ __device__ __forceinline__ i16x4 as_i16x4(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(i16x4, u);
 }
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2v;
+
+// acc + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs, fp32 accumulation.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a), __builtin_bit_cast(bf16x2v, b), acc,
+                                         false);
+}
+// Max / sum over the 16 lanes of each 16-lane row (DPP quad permutes, then row_half_mirror and
+// row_mirror, which pair quads and halves once those are uniform); every lane gets the result.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
 __device__ __forceinline__ void store_dump(const AttnParams& p, int64_t idx, float v) {
   if (p.dump_f32) {
     static_cast<float*>(p.dump)[idx] = v;
@@ -159,9 +191,10 @@ __device__ __forceinline__ void store_dump(const AttnParams& p, int64_t idx, flo
   }
 }
 
-template <int NT>
+template <int NT, bool kValu = false>
 __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it, int lane,
                                          i16x4 ident, bool staged, uint4* stage_lds) {
+  static_assert(!kValu || NT == 1, "the VALU path serves 1-tile items");
   constexpr bool kNtl = NT == 1 && ASPIRE_NT1_NTLOADS;
   const int r = lane & 15;
   const int grp = lane >> 4;
@@ -192,6 +225,36 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       for (int c = 0; c < 4; ++c) qf[t][c] = as_bf16x8(make_uint4(0, 0, 0, 0));
       limit[t] = -1;
       row_qi[t] = -1;
+    }
+  }
+
+  // VALU rows: every lane holds each row's q for its own 32 dims (4 chunks of 8); S is
+  // summed over the 4 dim groups with permlane swaps and maximised over the 16 keys with
+  // DPP; P.V accumulates in each lane for its key slot r and is summed over the 16 key
+  // lanes once, after the last page (the online-softmax rescale is uniform over keys).
+  uint4 qv[kValuRows][4];
+  int vlim[kValuRows];
+  float vm[kValuRows], vl[kValuRows];
+  float4 vacc[kValuRows][4][2];
+  if constexpr (kValu) {
+#pragma unroll
+    for (int j = 0; j < kValuRows; ++j) {
+      const int qi = j / G;
+      if (j < rows) {
+        const uint16_t* src =
+            p.q + int64_t(it.q_start + qi) * p.q_st + int64_t(g * G + (j - qi * G)) * p.q_sh;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qv[j][c] = load16(src + dim_off(grp, c));
+        vlim[j] = p.causal ? min(kv_len - it.q_len + qi, kv_len - 1) : kv_len - 1;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qv[j][c] = make_uint4(0, 0, 0, 0);
+        vlim[j] = -1;
+      }
+      vm[j] = kNegInf;
+      vl[j] = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) vacc[j][c][0] = vacc[j][c][1] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
 
@@ -241,6 +304,96 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   // here) or its V^T fragments ready for the PV MFMA (i16x4[8], one per
   // 16-dim slice j, read transposed from LDS).
   auto page_body = [&](int pg, const uint4 (&kr)[4], const auto& vsrc, auto&& after_qk, auto&& after_pv) {
+    if constexpr (kValu) {
+      float sv[kValuRows];
+#pragma unroll
+      for (int j = 0; j < kValuRows; ++j) {
+        float a = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          a = dot2_bf16(kr[c].x, qv[j][c].x, a);
+          a = dot2_bf16(kr[c].y, qv[j][c].y, a);
+          a = dot2_bf16(kr[c].z, qv[j][c].z, a);
+          a = dot2_bf16(kr[c].w, qv[j][c].w, a);
+        }
+        sv[j] = a;
+      }
+      after_qk();
+      // the 4 dim groups' partial dot products: every lane now holds q_j . k_r in full
+#pragma unroll
+      for (int j = 0; j < kValuRows; ++j) sv[j] = add_xor32(add_xor16(sv[j]));
+      const int key = pg * 16 + r;
+      if (do_dump && grp < rows) {
+        const int qi = grp / G;
+        int slot = -1;
+        if (p.dump_kind == 2)
+          slot = qi == 0 ? 0 : (qi == it.q_len - 1 ? 1 : -1);
+        else if (qi == it.q_len - 1)
+          slot = 0;
+        if (slot >= 0 && key < kv_len) {
+          const int head = g * G + (grp - qi * G);
+          const float v = grp == 0 ? sv[0] : grp == 1 ? sv[1] : grp == 2 ? sv[2] : sv[3];
+          store_dump(p, (int64_t(b * p.dump_heads + head) * dump_slots + slot) * p.dump_stride + key, v);
+        }
+      }
+      if (do_score) {
+        // key-mean score of this page: max over the group's heads of sum_{valid keys} q.k / count
+        const int cnt = min(16, kv_len - pg * 16);
+        float val = kNegInf;
+#pragma unroll
+        for (int j = 0; j < kValuRows; ++j) {
+          if (j < rows) {
+            const float rs = row16_sum(key < kv_len ? sv[j] : 0.f);
+            val = fmaxf(val, cnt == 16 ? rs * 0.0625f : rs / float(cnt));
+          }
+        }
+        const int slot = (pg - pb) & 63;
+        score_buf = lane == slot ? val : score_buf;
+        if (slot == 63 || pg == pe - 1) {
+          if (lane <= slot) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + (pg - slot) + lane] = score_buf;
+        }
+      }
+      float pr[kValuRows], alpha[kValuRows];
+      bool moved = false;
+#pragma unroll
+      for (int j = 0; j < kValuRows; ++j) {
+        const float x = key <= vlim[j] ? sv[j] * p.scale_log2 : kNegInf;
+        const float m_new = fmaxf(vm[j], row16_max(x));
+        float a = 1.f, e = 0.f;
+        if (m_new != kNegInf) {
+          a = __builtin_amdgcn_exp2f(vm[j] - m_new);
+          e = __builtin_amdgcn_exp2f(x - m_new);
+        }
+        vl[j] = vl[j] * a + e;  // this lane's key slot only; summed over the 16 keys at the end
+        vm[j] = m_new;
+        alpha[j] = a;
+        pr[j] = e;
+        moved |= a != 1.f;
+      }
+      if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+        for (int j = 0; j < kValuRows; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            vacc[j][c][0] *= alpha[j];
+            vacc[j][c][1] *= alpha[j];
+          }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint4 v = vsrc[c];
+        const float4 lo = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                                      __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+        const float4 hi = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                                      __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u));
+#pragma unroll
+        for (int j = 0; j < kValuRows; ++j) {
+          vacc[j][c][0] += pr[j] * lo;
+          vacc[j][c][1] += pr[j] * hi;
+        }
+      }
+      after_pv();
+    } else {
       const int base_pos = pg * 16 + grp * 4;
 
       f32x4 s[NT];
@@ -352,6 +505,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
         for (int t = 0; t < NT; ++t) acc[t][j] = mfma_16x16x16_bf16(vt, pf[t], acc[t][j]);
       }
       after_pv();
+    }
   };
 
   if constexpr (NT <= ASPIRE_STAGED_MAX_NT) {
@@ -493,6 +647,56 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     } while (++pg < pe);
   }
 
+  if constexpr (kValu) {
+    // sum the per-key-slot partials over the 16 key lanes of each dim group; lane (r, grp)
+    // then writes row r / 4's dims dim_off(grp, r % 4) .. + 8
+    const int jr = r >> 2, cr = r & 3;
+    float lt = 0.f, mt = kNegInf;
+    float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+#pragma unroll
+    for (int j = 0; j < kValuRows; ++j) {
+      const float lj = row16_sum(vl[j]);
+      if (j == jr) {
+        lt = lj;
+        mt = vm[j];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float4 a0 = vacc[j][c][0], a1 = vacc[j][c][1];
+        a0.x = row16_sum(a0.x); a0.y = row16_sum(a0.y); a0.z = row16_sum(a0.z); a0.w = row16_sum(a0.w);
+        a1.x = row16_sum(a1.x); a1.y = row16_sum(a1.y); a1.z = row16_sum(a1.z); a1.w = row16_sum(a1.w);
+        if (j == jr && c == cr) {
+          o0 = a0;
+          o1 = a1;
+        }
+      }
+    }
+    if (jr < rows) {
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      const float lse_v = lt > 0.f ? mt + __builtin_log2f(lt) : kNegInf;
+      const int qi = jr / G;
+      const int head = g * G + (jr - qi * G);
+      if (it.partial_row < 0) {
+        const int token = it.q_start + qi;
+        uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + dim_off(grp, cr);
+        uint4 w;
+        w.x = pack_bf16x2_rne(o0.x * inv, o0.y * inv);
+        w.y = pack_bf16x2_rne(o0.z * inv, o0.w * inv);
+        w.z = pack_bf16x2_rne(o1.x * inv, o1.y * inv);
+        w.w = pack_bf16x2_rne(o1.z * inv, o1.w * inv);
+        *reinterpret_cast<uint4*>(dst) = w;
+        if (grp == 0 && cr == 0 && p.lse != nullptr) p.lse[int64_t(token) * p.hq + head] = lse_v;
+      } else {
+        const int64_t prow = int64_t(it.partial_row) + jr;
+        float* dst = p.part_o + prow * kHeadDim + dim_off(grp, cr);
+        reinterpret_cast<float4*>(dst)[0] = make_float4(o0.x * inv, o0.y * inv, o0.z * inv, o0.w * inv);
+        reinterpret_cast<float4*>(dst)[1] = make_float4(o1.x * inv, o1.y * inv, o1.z * inv, o1.w * inv);
+        if (grp == 0 && cr == 0) p.part_lse[prow] = lse_v;
+      }
+    }
+    return;
+  }
+
   // Epilogue: normalise and write the final output or the fp32 partial.
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -555,7 +759,14 @@ __device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, 
     it.partial_row = wave_uniform(items[w].partial_row);
     // the flag is a property of the row, so the workgroup's 4 waves (heads of one
     // slot, walking the same rows) all take the same path
-    run_item<NT>(p, it, lane, ident, staged && !(q_len_flags & kItemDirect), stage_lds);
+    const bool stg = staged && !(q_len_flags & kItemDirect);
+    if constexpr (NT == 1 && ASPIRE_DRAFT_VALU) {
+      if (it.q_len * p.group <= kValuRows) {
+        run_item<1, true>(p, it, lane, ident, stg, stage_lds);
+        continue;
+      }
+    }
+    run_item<NT>(p, it, lane, ident, stg, stage_lds);
   }
 }
 

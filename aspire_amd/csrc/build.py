@@ -46,8 +46,8 @@ def source_digest() -> str:
     return h.hexdigest()
 
 
-def compile_one(src: str, defines: list[str]) -> Path:
-    obj = BUILD / (src + ".o")
+def compile_one(src: str, defines: list[str], build_dir: Path = BUILD) -> Path:
+    obj = build_dir / (src + ".o")
     cmd = [hipcc(), *COMMON, *defines, "-c", str(HERE / src), "-o", str(obj)]
     if src.endswith(".hip"):
         cmd[1:1] = ["-x", "hip", *DEVICE]
@@ -61,28 +61,40 @@ def compile_one(src: str, defines: list[str]) -> Path:
     return obj
 
 
-def build(jobs: int | None = None) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build(jobs: int | None = None, extra_defines: list[str] | None = None, out: Path | None = None) -> Path:
+    """Compile every source and link the library (``out``, default the in-tree library).
+    ``extra_defines`` (``NAME=VALUE``) select compile-time variants of the kernels, e.g.
+    ``ASPIRE_DRAFT_VALU=1``; such a build goes to its own ``out`` and its objects to their
+    own folder, so the default library is untouched."""
+    extra = [f"-D{d}" for d in (extra_defines or [])]
+    lib = Path(out) if out is not None else LIB
+    build_dir = BUILD if not extra else BUILD / ("variant_" + hashlib.sha256(" ".join(extra).encode()).hexdigest()[:12])
+    build_dir.mkdir(parents=True, exist_ok=True)
     digest = source_digest()
-    flags = " ".join(COMMON + DEVICE).replace('"', "")
-    defines = [f'-DASPIRE_SOURCE_SHA256="{digest}"', f'-DASPIRE_BUILD_FLAGS="{flags}"']
+    flags = " ".join(COMMON + DEVICE + extra).replace('"', "")
+    defines = [f'-DASPIRE_SOURCE_SHA256="{digest}"', f'-DASPIRE_BUILD_FLAGS="{flags}"', *extra]
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: compile_one(s, defines), SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda s: compile_one(s, defines, build_dir), SOURCES))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--define", action="append", default=[],
+                    help="NAME=VALUE compile-time variant (repeatable); needs --out")
+    ap.add_argument("--out", type=Path, default=None, help="library path for a variant build")
     args = ap.parse_args()
-    print(build(args.jobs))
+    if args.define and args.out is None:
+        ap.error("a variant build (--define) needs its own --out library path")
+    print(build(args.jobs, args.define, args.out))
 
 
 if __name__ == "__main__":

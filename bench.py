@@ -66,9 +66,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=1, choices=[1, 2, 3],
+    ap.add_argument("--config", type=int, default=1, choices=[1, 2, 3, 4],
                     help="1: mixed layer (default, also runs the components, config 4 and the config-3 decode "
-                         "step); 2: refresh layer; 3: the full 36-layer decode step alone")
+                         "step); 2: refresh layer; 3: the full 36-layer decode step alone; 4: the long-context "
+                         "layer at --draft-frac")
+    ap.add_argument("--draft-frac", type=float, default=0.5, help="config 4: fraction of drafting rows")
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed CPU-baseline runs per config (after 2 warm-ups)")
@@ -194,7 +196,7 @@ def main():
     from aspire_amd import _lib
     from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
     from aspire_amd.backends.page_selector import KeyMeanPageSelector
-    from aspire_amd.workloads import PAGE, config1, config2
+    from aspire_amd.workloads import PAGE, config1, config2, config4
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -212,7 +214,12 @@ def main():
         print(json.dumps(line), flush=True)
         return
     t0 = time.time()
-    step = config1(device=dev) if args.config == 1 else config2(device=dev)
+    if args.config == 1:
+        step = config1(device=dev)
+    elif args.config == 2:
+        step = config2(device=dev)
+    else:
+        step = config4(device=dev, draft_frac=args.draft_frac)
     torch.cuda.synchronize()
     log(f"workload built in {time.time() - t0:.1f}s: batch {step.batch}, tokens {step.total_tokens}, "
         f"pool {step.cache.shape[0]} pages ({step.cache.numel() * 2 / 2**30:.2f} GiB)")
@@ -246,6 +253,9 @@ def main():
         def run_step():
             w.run(step.q, cache, out=out, page_scores=selector.page_scores)
             selector.select(npg, step.block_table)
+    elif args.config == 4:
+        def run_step():
+            w.run(step.q, cache, out=out)
     else:
         def run_step():
             torch.ops.mylib.update_kv_padded(step.k_new, step.v_new, step.qo_indptr, cache, step.kv_indices,
@@ -298,10 +308,15 @@ def main():
                     "batch 32 x 32768-token contexts, 16 draft rows (q_len 1 over 128 selected pages) + 16 verify "
                     "rows (q_len 4, causal, full cache); KV append of the 80 new tokens + attention")
         metric = "mixed-attn layer HBM GB/s (Qwen3-8B shape, B=32 x 32k, 16 draft + 16 verify)"
-    else:
+    elif args.config == 2:
         workload = ("config2: Qwen3-8B-shape refresh layer, batch 64, contexts U[8192, 32768], full attention for "
                     "64 single-query rows + per-KV-head key-mean page scores + top-128 selection")
         metric = "refresh-layer HBM GB/s (Qwen3-8B shape, B=64, ctx U[8k,32k])"
+    else:
+        workload = (f"config4: DS-Llama-8B-shape long-context layer (32 q / 8 kv heads), batch 16, contexts "
+                    f"U[65536, 131072], draft fraction {args.draft_frac} (256-page drafts, verify q_len U{{2..9}}); "
+                    "attention + split-KV merge")
+        metric = f"long-context layer HBM GB/s (DS-Llama-8B shape, B=16, ctx U[64k,128k], f={args.draft_frac})"
     line = {
         "metric": metric,
         "value": round(value, 1),
@@ -333,7 +348,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "attention_kernel (mixed draft/verify, row-tile class 1)",
+            "kernel": "attention_kernel (mixed draft/verify persistent kernel, every row-tile class of the plan)",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
