@@ -105,7 +105,30 @@ constexpr int kStageRowChunks = 64;                      // 16-byte chunks per 1
 constexpr int kStageKv = 16 * kStageRowChunks;           // one of K / V
 constexpr int kStageBuf = 2 * kStageKv;                  // one buffer
 constexpr int kStageChunks = 2 * kStageBuf;              // 64 KiB
+// Per-wave V^T scratch of direct-load items (16 key rows x 16 chunks = 4 KiB per wave, when
+// ASPIRE_DIRECT_VT_MIN_NT enables it), after the stage buffers: a wave that has moved on to
+// a direct item never writes over stage buffers its workgroup's other waves may still read.
+constexpr int kVtChunks = 16 * 16;
 static_assert(kAttnWavesPerBlock == 4, "staged K/V assumes 4-wave workgroups (4 kv heads)");
+// Direct-load items with at least this many row tiles read V^T from the wave's LDS
+// scratch with transpose reads instead of transposing V rows with identity MFMAs. Off (4):
+// measured 1.7-2% slower on the long-context workload, because the V rows must be in LDS
+// before the softmax instead of before P.V, which puts the V wait on the critical path.
+#ifndef ASPIRE_DIRECT_VT_MIN_NT
+#define ASPIRE_DIRECT_VT_MIN_NT 4
+#endif
+constexpr int kLdsChunks = kStageChunks + (ASPIRE_DIRECT_VT_MIN_NT <= kMaxRowTiles ? kAttnWavesPerBlock * kVtChunks : 0);
+// Issue the next page's V load right after QK^T (with K's) rather than after P.V.
+#ifndef ASPIRE_DIRECT_VT_EARLY_V
+#define ASPIRE_DIRECT_VT_EARLY_V 0
+#endif
+
+// LDS row swizzle: 16-byte chunk c of key row r is stored at chunk c ^ swz(r). swz swaps
+// the two 2-bit halves of r, which keeps all three access patterns on distinct banks:
+// whole-row writes (one row, 64 consecutive chunks), the 16-row column reads of the MFMA
+// operand layout (rows 0..15, chunk 4c + grp) and the transpose reads of V^T (rows
+// 4grp + 0..3, chunks 4m + 0..3): (4m + k) ^ swz(4grp + q) = 4(m ^ q) + (k ^ grp).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | (r >> 2); }
 
 // LDS-only release/acquire around the workgroup barrier: waits for this
 // wave's LDS writes (lgkmcnt) but not for its K/V loads in flight.
@@ -518,8 +541,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       // LDS; after a barrier every wave reads its own head's rows from LDS in the
       // MFMA operand layout. Contiguous 1 KiB loads stream measurably faster
       // from HBM than 16 rows x 64 B per instruction. LDS chunk c of key row r
-      // sits at c ^ r, so the row writes and the 16-row column reads both hit 16
-      // different bank groups. Two LDS buffers: page pg is read from one while
+      // sits at c ^ swz(r), so row writes, column reads and transpose reads are all
+      // free of bank conflicts. Two LDS buffers: page pg is read from one while
       // page pg + 1 is stored to the other and page pg + 2 is in flight.
       if (pb < pe) {
         const int wl = (threadIdx.x >> 6) & 3;
@@ -541,13 +564,13 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             const int row = r0 + i;
-            base[row * kStageRowChunks + (lane ^ row)] = st[i];
+            base[row * kStageRowChunks + (lane ^ swz(row))] = st[i];
           }
         };
         auto read_rows = [&](int buf, int kv, uint4(&dst)[4]) {
           const uint4* base = stage_lds + buf * kStageBuf + kv * kStageKv + r * kStageRowChunks;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) dst[c] = base[(gl * 16 + c * 4 + grp) ^ r];
+          for (int c = 0; c < 4; ++c) dst[c] = base[(gl * 16 + c * 4 + grp) ^ swz(r)];
         };
         // V^T fragments straight from the staged rows with the LDS transpose
         // read: of the 16 lanes of group grp, lane r addresses key row
@@ -561,7 +584,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
                                                            vt_row * kStageRowChunks);
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const int chunk = (gl * 16 + 4 * (j >> 1) + (r & 3)) ^ vt_row;
+            const int chunk = (gl * 16 + 4 * (j >> 1) + (r & 3)) ^ swz(vt_row);
             vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) i16x4*)(base + chunk * 16 + 8 * (j & 1)));
           }
@@ -636,15 +659,55 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     }
     int64_t id_ahead = page_id(pb + 1);
     int pg = pb;
-    do {
-      const bool has_next = pg + 1 < pe;
-      const int64_t next_phys = id_ahead;
-      id_ahead = page_id(pg + 2);
-      // Issued unconditionally (straight-line code keeps the wait counts
-      // exact); past the item's last page the out-of-range offset returns zeros.
-      const bool next_ok = has_next && (pg + 1) * 16 + r < kv_len;
-      page_body(pg, kr, vr, [&] { load_k(next_phys, next_ok, kr); }, [&] { load_v(next_phys, next_ok, vr); });
-    } while (++pg < pe);
+    if constexpr (!kValu && NT >= ASPIRE_DIRECT_VT_MIN_NT) {
+      // V^T through the wave's LDS scratch: the page's V rows (keys past kv_len arrive as
+      // zeros) are written in the swizzled row layout and read back transposed, the PV
+      // MFMA's A operand. Both next-page loads are issued once QK^T has consumed K and the
+      // V rows are in LDS, so two loads are in flight during the softmax. LDS operations
+      // of one wave complete in order, so the read after the write and the next page's
+      // write after this page's reads need no wait.
+      uint4* vt_lds = stage_lds + kStageChunks + ((threadIdx.x >> 6) & (kAttnWavesPerBlock - 1)) * kVtChunks;
+      const int vt_row = 4 * grp + (r >> 2);
+      do {
+        const bool has_next = pg + 1 < pe;
+        const int64_t next_phys = id_ahead;
+        id_ahead = page_id(pg + 2);
+        const bool next_ok = has_next && (pg + 1) * 16 + r < kv_len;
+        i16x4 vt[8];
+        page_body(
+            pg, kr, vt,
+            [&] {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) vt_lds[r * 16 + ((4 * c + grp) ^ swz(r))] = vr[c];
+              const char* base = reinterpret_cast<const char*>(vt_lds + vt_row * 16);
+#pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                const int chunk = (4 * (j >> 1) + (r & 3)) ^ swz(vt_row);
+                vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) i16x4*)(base + chunk * 16 + 8 * (j & 1)));
+              }
+              load_k(next_phys, next_ok, kr);
+#if ASPIRE_DIRECT_VT_EARLY_V
+              load_v(next_phys, next_ok, vr);
+#endif
+            },
+            [&] {
+#if !ASPIRE_DIRECT_VT_EARLY_V
+              load_v(next_phys, next_ok, vr);
+#endif
+            });
+      } while (++pg < pe);
+    } else {
+      do {
+        const bool has_next = pg + 1 < pe;
+        const int64_t next_phys = id_ahead;
+        id_ahead = page_id(pg + 2);
+        // Issued unconditionally (straight-line code keeps the wait counts
+        // exact); past the item's last page the out-of-range offset returns zeros.
+        const bool next_ok = has_next && (pg + 1) * 16 + r < kv_len;
+        page_body(pg, kr, vr, [&] { load_k(next_phys, next_ok, kr); }, [&] { load_v(next_phys, next_ok, vr); });
+      } while (++pg < pe);
+    }
   }
 
   if constexpr (kValu) {
@@ -790,7 +853,7 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
   // the 4 waves of a workgroup the same pages: their 1-tile items stage K/V
   // through LDS. The flag is uniform over the workgroup, so every wave takes
   // the same barriers.
-  __shared__ uint4 stage_lds[kStageChunks];
+  __shared__ uint4 stage_lds[kLdsChunks];
   const int hpu = wave_uniform(p.plan[4]);
   const bool staged = p.staged_ok && hpu > 0 && hpu % 4 == 0;
   if (p.class_mask & 1) run_class<1>(p, 0, wave, lane, ident, staged, stage_lds);
