@@ -51,6 +51,8 @@ EXPORTED = (
     "aspire_sampling_from_probs",
     "aspire_chain_speculative_sampling",
     "aspire_verify_topk_speculation",
+    "aspire_prefill_block_tokens",
+    "aspire_prefill_run",
 )
 
 # Bytes of the static device scratch behind aspire_attention_run_static (ASPIRE_STATIC_SCRATCH_BYTES).
@@ -101,6 +103,21 @@ class AttentionArgs(ctypes.Structure):
         ("dump_kv_stride", ctypes.c_int64), ("dump_num_heads", ctypes.c_int32),
         ("dump_mode_flags", ctypes.c_void_p),
         ("page_scores", ctypes.c_void_p), ("page_score_stride", ctypes.c_int64),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_stride_t", ctypes.c_int64), ("q_stride_h", ctypes.c_int64),
+        ("kv_cache", ctypes.c_void_p), ("cache_stride_p", ctypes.c_int64), ("cache_stride_kv", ctypes.c_int64),
+        ("cache_stride_t", ctypes.c_int64), ("cache_stride_h", ctypes.c_int64),
+        ("kv_indices", ctypes.c_void_p), ("kv_indptr", ctypes.c_void_p), ("kv_last_page_len", ctypes.c_void_p),
+        ("qo_indptr", ctypes.c_void_p), ("block_indptr", ctypes.c_void_p),
+        ("num_rows", ctypes.c_int32), ("total_blocks", ctypes.c_int32), ("block_tokens", ctypes.c_int32),
+        ("out", ctypes.c_void_p), ("out_stride_t", ctypes.c_int64), ("out_stride_h", ctypes.c_int64),
+        ("lse", ctypes.c_void_p),
+        ("num_qo_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("page_size", ctypes.c_int32), ("sm_scale", ctypes.c_float), ("causal", ctypes.c_int32),
     ]
 
 
@@ -198,6 +215,8 @@ def _declare(lib):
         "aspire_sampling_from_probs": [vp, i64, i32, i32, vp, vp, vp],
         "aspire_chain_speculative_sampling": [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp],
         "aspire_verify_topk_speculation": [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
+        "aspire_prefill_block_tokens": [i32, i32],
+        "aspire_prefill_run": [ctypes.POINTER(PrefillArgs), vp],
     }
     for name, argtypes in sigs.items():
         fn = getattr(lib, name)

@@ -3,21 +3,26 @@
 The reference plans and runs FlashInfer's paged prefill wrapper for prompt chunks
 (aspire/models/sparse_draft_runner.py:199-209; the chunk loop of ``encode_slots``,
 aspire/backends/base.py:1559-1674): causal attention of each row's new tokens over its
-cached prefix plus the new tokens, page lists as for decode. Here it is the same HIP
-kernel and planner as the mixed decode path: rows longer than one 48-query-row item are
-cut by the planner into query tiles whose keys end at the tile's last token. ``plan`` /
-``run`` keep FlashInfer's names and argument meanings; options this path does not
-implement (custom masks, sliding windows, logit soft caps, fused RoPE) raise
-``ValueError``.
+cached prefix plus the new tokens, page lists as for decode. ``run`` launches the
+dedicated prefill kernel (``aspire_prefill_run``): each workgroup takes one query block
+(``aspire_prefill_block_tokens(hq, hkv)`` tokens of one row, all G query heads of one kv
+head) and stages every page of its keys once in LDS, two pages per step, for all of its
+waves. ``kernel="decode"`` runs the mixed decode kernel and its
+planner instead (rows cut into 48-query-row tiles). ``plan`` / ``run`` keep FlashInfer's
+names and argument meanings; options this path does not implement (custom masks, sliding
+windows, logit soft caps, fused RoPE) raise ``ValueError``.
 """
 
 from __future__ import annotations
 
+import ctypes
+import math
 from typing import Optional, Union
 
 import torch
 
-from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
+from aspire_amd import _lib
+from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper, _unpack_paged_kv_cache
 
 
 class BatchPrefillWithPagedKVCacheWrapper(HolisticAttentionWrapper):
@@ -25,7 +30,12 @@ class BatchPrefillWithPagedKVCacheWrapper(HolisticAttentionWrapper):
                  qo_indptr_buf: Optional[torch.Tensor] = None, paged_kv_indptr_buf: Optional[torch.Tensor] = None,
                  paged_kv_indices_buf: Optional[torch.Tensor] = None,
                  paged_kv_last_page_len_buf: Optional[torch.Tensor] = None, backend: str = "auto",
-                 jit_args: Optional[list] = None, jit_kwargs: Optional[dict] = None, **kwargs):
+                 jit_args: Optional[list] = None, jit_kwargs: Optional[dict] = None, *, kernel: str = "prefill",
+                 **kwargs):
+        if kernel not in ("prefill", "decode"):
+            raise ValueError("kernel must be 'prefill' or 'decode'")
+        self._kernel = kernel
+        self._pf = None
         super().__init__(float_workspace_buffer, kv_layout, use_cuda_graph=use_cuda_graph,
                          qo_indptr_buf=qo_indptr_buf, paged_kv_indptr_buf=paged_kv_indptr_buf,
                          paged_kv_indices_buf=paged_kv_indices_buf,
@@ -49,15 +59,77 @@ class BatchPrefillWithPagedKVCacheWrapper(HolisticAttentionWrapper):
         super().plan(qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len, num_qo_heads,
                      num_kv_heads, head_dim_qk, page_size, head_dim_vo=head_dim_vo, q_data_type=q_data_type,
                      causal=causal, sm_scale=sm_scale)
+        self._pf = None
+        if self._kernel != "prefill" or self._has_jit:
+            return
+        bt = int(_lib.lib().aspire_prefill_block_tokens(num_qo_heads, num_kv_heads))
+        if bt <= 0:
+            raise ValueError("the prefill kernel does not take this head group (num_qo_heads / num_kv_heads must "
+                             "divide a wave's 16 query rows); plan with kernel='decode'")
+        # rows: the entries of kv_last_page_len (FlashInfer's batch), with their query blocks
+        n = paged_kv_last_page_len.shape[0]
+        qo_host = qo_indptr[: n + 1].to("cpu", torch.int64)
+        q_len = (qo_host[1:] - qo_host[:-1]).clamp(min=0)
+        blocks = torch.zeros(n + 1, dtype=torch.int64)
+        blocks[1:] = torch.cumsum((q_len + bt - 1) // bt, 0)
+        dev = paged_kv_indices.device
+        self._pf = {
+            "qo": qo_indptr[: n + 1].to(dev, torch.int32).contiguous(),
+            "kvp": paged_kv_indptr[: n + 1].to(dev, torch.int32).contiguous(),
+            "lpl": paged_kv_last_page_len[:n].to(dev, torch.int32).contiguous(),
+            "idx": paged_kv_indices.to(torch.int32).contiguous(),
+            "blocks": blocks.to(dev, torch.int32),
+            "rows": n, "total_blocks": int(blocks[-1]), "block_tokens": bt,
+            "tokens": int(qo_host[-1]) if n else 0,
+        }
 
     def run(self, q: torch.Tensor, paged_kv_cache, *args, out: Optional[torch.Tensor] = None,
             lse: Optional[torch.Tensor] = None, return_lse: bool = False, **kwargs):
-        res = super().run(q, paged_kv_cache, *args, out=out, return_lse=True)
-        o, l_ = res
-        if lse is not None:
-            lse.copy_(l_)
-            l_ = lse
-        return (o, l_) if return_lse else o
+        if self._pf is None:
+            res = super().run(q, paged_kv_cache, *args, out=out, return_lse=True)
+            o, l_ = res
+            if lse is not None:
+                lse.copy_(l_)
+                l_ = lse
+            return (o, l_) if return_lse else o
+        pf = self._pf
+        k_cache, v_cache = _unpack_paged_kv_cache(paged_kv_cache, self._kv_layout)
+        _lib.require_cuda(q, k_cache, v_cache, what="BatchPrefillWithPagedKVCacheWrapper.run")
+        if q.dim() != 3 or q.shape[2] != 128 or q.stride(2) != 1 or q.dtype != torch.bfloat16:
+            raise ValueError("q must be bf16 [T, num_qo_heads, 128] with a contiguous head dimension")
+        if q.shape[1] != self._num_qo_heads or q.shape[0] < pf["tokens"]:
+            raise ValueError("q's heads / tokens disagree with the plan")
+        if k_cache.dtype != torch.bfloat16 or k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
+            raise ValueError("kv_cache must be bf16 with k and v sharing strides and a contiguous head dimension")
+        if k_cache.shape[1] != self._page_size or k_cache.shape[2] != self._num_kv_heads:
+            raise ValueError("kv_cache page size / kv heads disagree with the plan")
+        if out is None:
+            out = torch.empty_like(q)
+        if out.shape != q.shape or out.stride(2) != 1 or out.dtype != q.dtype:
+            raise ValueError("out must match q's shape and dtype with a contiguous head dimension")
+        want_lse = return_lse or lse is not None
+        if lse is None and want_lse:
+            lse = torch.empty(q.shape[0], q.shape[1], device=q.device, dtype=torch.float32)
+        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
+                                or tuple(lse.shape) != (q.shape[0], q.shape[1])):
+            raise ValueError("lse must be a contiguous fp32 [T, num_qo_heads] tensor")
+        elem = k_cache.element_size()
+        a = _lib.PrefillArgs()
+        a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+        a.kv_cache = k_cache.data_ptr()
+        a.cache_stride_p, a.cache_stride_kv = k_cache.stride(0), (v_cache.data_ptr() - k_cache.data_ptr()) // elem
+        a.cache_stride_t, a.cache_stride_h = k_cache.stride(1), k_cache.stride(2)
+        a.kv_indices, a.kv_indptr = pf["idx"].data_ptr(), pf["kvp"].data_ptr()
+        a.kv_last_page_len, a.qo_indptr, a.block_indptr = pf["lpl"].data_ptr(), pf["qo"].data_ptr(), pf["blocks"].data_ptr()
+        a.num_rows, a.total_blocks, a.block_tokens = pf["rows"], pf["total_blocks"], pf["block_tokens"]
+        a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+        a.lse = lse.data_ptr() if lse is not None else None
+        a.num_qo_heads, a.num_kv_heads, a.head_dim, a.page_size = self._num_qo_heads, self._num_kv_heads, 128, 16
+        a.sm_scale = float(self._sm_scale if self._sm_scale is not None else 1.0 / math.sqrt(128))
+        a.causal = 1 if self._causal else 0
+        rc = _lib.lib().aspire_prefill_run(ctypes.byref(a), _lib.stream_of(q))
+        _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.run")
+        return (out, lse) if return_lse else out
 
     forward = run
 

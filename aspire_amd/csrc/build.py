@@ -22,7 +22,7 @@ PKG = HERE.parent
 LIB = PKG / "libaspire_hip.so"
 BUILD = HERE / "_build"
 SOURCES = ["capi.cpp", "plan.cpp", "host_plan.cpp", "append.hip", "page_list.hip", "attention.hip", "select.hip",
-           "rope_append.hip", "decode_ops.hip", "sampling.hip"]
+           "rope_append.hip", "decode_ops.hip", "sampling.hip", "prefill.hip"]
 ARCH = "gfx950"
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function"]
@@ -46,9 +46,14 @@ def source_digest() -> str:
     return h.hexdigest()
 
 
+# Per-source flags. prefill.hip: IEEE mode off, so fp32 max needs no NaN-quieting
+# canonicalisation of MFMA results (its scores are never NaN once masked).
+FILE_FLAGS = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"]}
+
+
 def compile_one(src: str, defines: list[str], build_dir: Path = BUILD) -> Path:
     obj = build_dir / (src + ".o")
-    cmd = [hipcc(), *COMMON, *defines, "-c", str(HERE / src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON, *FILE_FLAGS.get(src, []), *defines, "-c", str(HERE / src), "-o", str(obj)]
     if src.endswith(".hip"):
         cmd[1:1] = ["-x", "hip", *DEVICE]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,414 @@
+// (f3) Chunked-prefill paged attention for gfx950.
+//
+// A workgroup of kPfWaves waves takes one query block of one (row, kv head): kPfWaves x 16 x
+// kPfTiles query rows (block_tokens = that / G tokens, G = q heads per kv head), 16 x kPfTiles
+// rows per wave. Every page of the block's keys is read from HBM once per workgroup: the
+// waves load two pages at a time (K and V rows of this kv head, 16 KiB) into a
+// double-buffered LDS stage and each wave then runs its tiles over those 32 keys:
+//   * S^T = K . Q^T per page and tile with 4 v_mfma_f32_16x16x32_bf16 (K rows from LDS in
+//     the swizzled layout, Q fragments in registers); lane (r, grp) holds S^T[key 4grp + i][row r];
+//   * online softmax in fp32 over the 32 keys (exp2 with the scale folded into its argument,
+//     base-2 LSE; row max across the 4 lane groups with permlane swaps), causal masking only
+//     on steps that reach a row's limit, accumulator rescale only when some row's max moved;
+//   * O^T += V^T . P^T with 8 v_mfma_f32_16x16x32_bf16 per tile: each lane's 8 keys are
+//     keys 4grp..4grp+3 of both pages (the order S^T left them in), V^T comes from LDS with
+//     transpose reads (ds_read_b64_tr_b16) and is shared by the wave's tiles.
+// The grid is 1-D with the kv head fastest: the last query blocks of every head (the most
+// keys under a causal mask) start first, and with num_kv_heads a multiple of 8 the
+// round-robin spread of workgroups over the 8 XCDs keeps each head's pages in one L2.
+// Waves whose tokens end before a step skip its compute but keep staging.
+#include "common.h"
+
+namespace aspire {
+namespace {
+
+constexpr float kNegInfP = -__builtin_huge_valf();
+#ifndef ASPIRE_PF_WAVES
+#define ASPIRE_PF_WAVES 8
+#endif
+#ifndef ASPIRE_PF_TILES
+#define ASPIRE_PF_TILES 1
+#endif
+constexpr int kPfWaves = ASPIRE_PF_WAVES;   // waves per workgroup
+constexpr int kPfTiles = ASPIRE_PF_TILES;   // 16-row query tiles per wave
+constexpr int kPfRows = 16 * kPfTiles;      // query rows per wave
+constexpr int kPfBlockRows = kPfWaves * kPfRows;
+constexpr int kPfThreads = 64 * kPfWaves;
+#ifndef ASPIRE_PF_WAVES_PER_EU
+#define ASPIRE_PF_WAVES_PER_EU ((ASPIRE_PF_WAVES + 3) / 4)
+#endif
+constexpr int kPfWavesPerEu = ASPIRE_PF_WAVES_PER_EU;  // register budget: waves per SIMD
+constexpr int kPfRowChunks = 16;            // 16-byte chunks per 256-byte key row (one kv head)
+constexpr int kPfHalf = 16 * kPfRowChunks;  // K or V rows of one page, in chunks
+constexpr int kPfPage = 2 * kPfHalf;        // one page: K rows, then V rows
+constexpr int kPfStage = 2 * kPfPage;       // one step: two pages
+constexpr int kPfStepKeys = 2 * kPage;      // keys per step
+
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4p;
+constexpr uint32_t kPfBufferConfig = 0x00020000u;  // gfx9 raw buffer dword 3
+constexpr int kPfOutOfRange = 0x7ffffff0;          // an offset past every descriptor's range
+static_assert(kPfThreads % 64 == 0 && 1024 % kPfThreads == 0, "a step's chunks split evenly over the threads");
+
+// A pointer the whole wave agrees on, kept in scalar registers (buffer descriptors need that).
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(const T* ptr) {
+  const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v)), hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+  return reinterpret_cast<T*>((uint64_t(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ int pf_swz(int r) { return ((r & 3) << 2) | (r >> 2); }
+
+__device__ __forceinline__ i16x4 pf_i16x4(uint32_t a, uint32_t b) {
+  uint2 u = make_uint2(a, b);
+  return __builtin_bit_cast(i16x4, u);
+}
+
+struct PrefillParams {
+  const uint16_t* q;
+  int64_t q_st, q_sh;
+  const uint16_t* cache;
+  int64_t c_sp, c_skv, c_st, c_sh;
+  const int32_t* kv_indices;
+  const int32_t* kv_indptr;
+  const int32_t* last_page_len;
+  const int32_t* qo_indptr;
+  const int32_t* block_indptr;
+  int32_t num_rows, total_blocks, block_tokens;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  float* lse;
+  int32_t hq, group;
+  float scale_log2;
+  int32_t causal;
+};
+
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfWavesPerEu))) void prefill_kernel(
+    PrefillParams p) {
+  __shared__ uint4 stage[2 * kPfStage];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_uniform(threadIdx.x >> 6);
+  const int r = lane & 15, grp = lane >> 4;
+  const int G = p.group;
+
+  // (query block, kv head) of this workgroup: kv head fastest, so consecutive workgroups
+  // (spread over the XCDs round robin) keep one head per XCD when num_kv_heads is a
+  // multiple of 8, and the last query blocks of every head start first
+  const int hkv = p.hq / G;
+  const int g = wave_uniform(int(blockIdx.x) % hkv);
+  const int blk = wave_uniform(p.total_blocks - 1 - int(blockIdx.x) / hkv);
+  int lo = 0, hi = p.num_rows - 1, b = 0;
+  while (lo <= hi) {
+    const int mid = (lo + hi) >> 1;
+    if (p.block_indptr[mid] <= blk) {
+      b = mid;
+      lo = mid + 1;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  b = wave_uniform(b);
+  const int qb = blk - p.block_indptr[b];
+  const int q0 = p.qo_indptr[b];
+  const int q_len = p.qo_indptr[b + 1] - q0;
+  const int list0 = p.kv_indptr[b];
+  const int np = p.kv_indptr[b + 1] - list0;
+  const int kv_len = max(np - 1, 0) * kPage + p.last_page_len[b];
+  const int tpw = kPfRows / G;  // tokens per wave
+  const int tok0 = qb * p.block_tokens;
+  const int ntok = min(p.block_tokens, q_len - tok0);
+  const int wt0 = tok0 + wave * tpw;
+  const int wn = max(0, min(tpw, q_len - wt0));
+  const int rows = wn * G;
+  // keys of the block (all waves stage them) and of this wave
+  const int shift = kv_len - q_len;
+  const int blk_last = p.causal ? min(shift + tok0 + ntok - 1, kv_len - 1) : kv_len - 1;
+  const int blk_pages = blk_last >= 0 ? blk_last / kPage + 1 : 0;
+  const int steps = wave_uniform((blk_pages + 1) / 2);
+  const int vlim = wave_uniform(min(kv_len, blk_pages * kPage));
+  const int w_last = wave_uniform(rows > 0 ? (p.causal ? min(shift + wt0 + wn - 1, kv_len - 1) : kv_len - 1) : -1);
+  const int w_min_limit = wave_uniform(p.causal ? min(shift + wt0, kv_len - 1) : kv_len - 1);
+
+  // Q fragments (B operand of S^T = K . Q^T) and causal limits of the wave's rows
+  bf16x8 qf[kPfTiles][4];
+  int limit[kPfTiles];
+#pragma unroll
+  for (int t = 0; t < kPfTiles; ++t) {
+    const int row = t * 16 + r;
+    if (row < rows) {
+      const int ti = row / G;
+      const int hh = row - ti * G;
+      const uint16_t* src = p.q + int64_t(q0 + wt0 + ti) * p.q_st + int64_t(g * G + hh) * p.q_sh;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qf[t][c] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(src + 32 * c + 8 * grp));
+      limit[t] = p.causal ? min(shift + wt0 + ti, kv_len - 1) : kv_len - 1;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qf[t][c] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+      limit[t] = -1;
+    }
+  }
+  float m[kPfTiles], l[kPfTiles];
+  f32x4 acc[kPfTiles][8];
+#pragma unroll
+  for (int t = 0; t < kPfTiles; ++t) {
+    m[t] = kNegInfP;
+    l[t] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Staging. A step's 1024 chunks (16 B) are 4 kinds of 256: page 2s K rows, its V rows, page
+  // 2s + 1 K rows, V rows. Thread t moves chunks t + i * threads; a chunk's kind is uniform
+  // across each wave, so its source is one scalar buffer descriptor per (kind, page) and a
+  // fixed per-lane offset. Loads go through buffer descriptors: a chunk past vlim (stale slots
+  // past kv_len, pages the block does not reach) gets an offset beyond the descriptor's range
+  // and comes back as zeros, so the P.V loop needs no masks.
+  const int t = threadIdx.x;
+  const int crow = (t & 255) >> 4, ccol = t & 15;
+  const int voff = crow * int(p.c_st) * 2 + ccol * 16;
+  const int lds_off = (t & 255 & ~15) + (ccol ^ pf_swz(crow));
+  const int span = wave_uniform(15 * int(p.c_st) * 2 + 256);
+  const __amdgpu_buffer_rsrc_t ids_rs = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(p.kv_indices + list0), (short)0, np * 4, kPfBufferConfig);
+  // page ids through vector loads (in order with the K/V loads, so their wait is exact)
+  auto page_ids = [&](int st_idx, int& ia, int& ib) {
+    ia = __builtin_amdgcn_raw_buffer_load_b32(ids_rs, 8 * st_idx, 0, 0);
+    ib = __builtin_amdgcn_raw_buffer_load_b32(ids_rs, 8 * st_idx + 4, 0, 0);
+  };
+  constexpr int kPer = kPfStage / kPfThreads;  // chunks per thread
+  auto issue = [&](int k, int ia, int ib, uint4(&st)[kPer]) {
+    const int64_t pa = wave_uniform(ia), pb = wave_uniform(ib);
+    const bool edge = k * kPfStepKeys + kPfStepKeys > vlim;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int kind = (wave * 64 + i * kPfThreads) >> 8;
+      const int64_t phys = (kind >> 1) ? pb : pa;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          uniform_ptr(p.cache + phys * p.c_sp + (kind & 1) * p.c_skv + int64_t(g) * p.c_sh), (short)0, span,
+          kPfBufferConfig);
+      int off = voff;
+      if (edge) off = k * kPfStepKeys + (kind >> 1) * kPage + crow < vlim ? voff : kPfOutOfRange;
+      const u32x4p v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+      st[i] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+  };
+  auto store = [&](int buf, const uint4(&st)[kPer]) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) stage[buf * kPfStage + ((wave * 64 + i * kPfThreads) >> 8) * kPfHalf + lds_off] = st[i];
+  };
+
+  const int vt_row = 4 * grp + (r >> 2);
+  auto compute = [&](int s) {
+    const int buf = s & 1;
+    const int key0 = s * kPfStepKeys;
+    // S^T of both pages: lane (r, grp) holds keys key0 + 4grp + i (sa) and key0 + 16 + 4grp + i (sb)
+    const uint4* kb = stage + buf * kPfStage;
+    f32x4 sa[kPfTiles], sb[kPfTiles];
+    {
+      uint4 kr[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kr[c] = kb[r * kPfRowChunks + ((4 * c + grp) ^ pf_swz(r))];
+#pragma unroll
+      for (int tt = 0; tt < kPfTiles; ++tt) {
+        sa[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sa[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sa[tt]);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kr[c] = kb[kPfPage + r * kPfRowChunks + ((4 * c + grp) ^ pf_swz(r))];
+#pragma unroll
+      for (int tt = 0; tt < kPfTiles; ++tt) {
+        sb[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sb[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sb[tt]);
+      }
+    }
+    // online softmax over the step's 32 keys; the scale is folded into exp2's argument. A row
+    // with no key yet (max -inf) uses 0 as its offset: its exponentials and alpha are all 0.
+    const int pos = key0 + grp * 4;
+    const bool need_mask = key0 + kPfStepKeys - 1 > w_min_limit;
+    bf16x8 pf[kPfTiles];
+    float alpha[kPfTiles];
+    bool moved = false;
+#pragma unroll
+    for (int tt = 0; tt < kPfTiles; ++tt) {
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = sa[tt][i];
+        x[4 + i] = sb[tt][i];
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[i] = (pos + i <= limit[tt]) ? x[i] : kNegInfP;
+          x[4 + i] = (pos + kPage + i <= limit[tt]) ? x[4 + i] : kNegInfP;
+        }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      mx = max_xor32(max_xor16(mx));
+      const float m_new = fmaxf(m[tt], mx * p.scale_log2);
+      const float m_use = m_new == kNegInfP ? 0.f : m_new;
+      const float a = __builtin_amdgcn_exp2f(m[tt] - m_use);
+      float pv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pv[i] = __builtin_amdgcn_exp2f(fmaf(x[i], p.scale_log2, -m_use));
+      l[tt] = l[tt] * a + (((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7])));
+      m[tt] = m_new;
+      alpha[tt] = a;
+      moved |= a != 1.f;
+      uint4 w;
+      w.x = pack_bf16x2_rne(pv[0], pv[1]);
+      w.y = pack_bf16x2_rne(pv[2], pv[3]);
+      w.z = pack_bf16x2_rne(pv[4], pv[5]);
+      w.w = pack_bf16x2_rne(pv[6], pv[7]);
+      pf[tt] = __builtin_bit_cast(bf16x8, w);
+    }
+    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+      for (int tt = 0; tt < kPfTiles; ++tt)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[tt][j] *= alpha[tt];
+    }
+    // O^T += V^T . P^T with 16x16x32 MFMAs over the step's 32 keys: lane (r, grp) carries keys
+    // 4grp..4grp+3 of both pages, the order P^T's fragment uses; V^T by transpose reads
+    const char* va = reinterpret_cast<const char*>(kb + kPfHalf + vt_row * kPfRowChunks);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int off = ((4 * (j >> 1) + (r & 3)) ^ pf_swz(vt_row)) * 16 + 8 * (j & 1);
+      const uint2 wa = __builtin_bit_cast(
+          uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(va + off)));
+      const uint2 wb = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                     (__attribute__((address_space(3))) i16x4*)(va + kPfPage * 16 + off)));
+      const bf16x8 vt = __builtin_bit_cast(bf16x8, make_uint4(wa.x, wa.y, wb.x, wb.y));
+#pragma unroll
+      for (int tt = 0; tt < kPfTiles; ++tt) acc[tt][j] = mfma_16x16x32_bf16(vt, pf[tt], acc[tt][j]);
+    }
+  };
+
+  // Pipeline: step s computes from LDS buffer s & 1; its K/V were loaded into registers at the
+  // start of step s - 2 (two steps to land) and stored at the end of step s - 1. The page ids
+  // of step s + 3 are loaded at the start of step s, ahead of that step's K/V loads.
+  // Every step issues the same loads (steps past the block read as zeros through the
+  // out-of-range offset), so the outstanding-load queue has one shape on every iteration:
+  // [ids(s + 2), K/V(s + 1)] at the top of step s.
+  if (steps > 0) {
+    uint4 st0[kPer], st1[kPer];
+    int i0a, i0b, i1a, i1b, na, nb;
+    page_ids(0, i0a, i0b);
+    page_ids(1, i1a, i1b);
+    issue(0, i0a, i0b, st0);
+    page_ids(2, na, nb);
+    issue(1, i1a, i1b, st1);
+    store(0, st0);
+    __syncthreads();
+    auto body = [&](int s, uint4(&st_issue)[kPer], uint4(&st_store)[kPer]) {
+      const int ca = na, cb = nb;
+      page_ids(s + 3, na, nb);
+      issue(s + 2, ca, cb, st_issue);
+      if (s < steps && s * kPfStepKeys <= w_last) compute(s);
+      if (s + 1 < steps) store((s + 1) & 1, st_store);
+      __syncthreads();
+    };
+    // two steps per trip, the second one possibly past the block (loads of zeros, no compute,
+    // no store): both halves keep one shape, so the loads in flight never force a wait early
+    for (int s = 0; s < steps; s += 2) {
+      body(s, st0, st1);
+      body(s + 1, st1, st0);
+    }
+  }
+
+  // epilogue: normalise, write bf16 rows and the base-2 LSE
+#pragma unroll
+  for (int tt = 0; tt < kPfTiles; ++tt) {
+    float lt = l[tt];
+    lt += shfl_xor_f(lt, 16);
+    lt += shfl_xor_f(lt, 32);
+    const int row = tt * 16 + r;
+    if (row >= rows) continue;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const float lse_v = lt > 0.f ? m[tt] + __builtin_log2f(lt) : kNegInfP;
+    const int ti = row / G;
+    const int head = g * G + (row - ti * G);
+    const int token = q0 + wt0 + ti;
+    uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x4 a0 = acc[tt][2 * c];
+      const f32x4 a1 = acc[tt][2 * c + 1];
+      uint4 w;
+      w.x = pack_bf16x2_rne(a0[0] * inv, a0[1] * inv);
+      w.y = pack_bf16x2_rne(a0[2] * inv, a0[3] * inv);
+      w.z = pack_bf16x2_rne(a1[0] * inv, a1[1] * inv);
+      w.w = pack_bf16x2_rne(a1[2] * inv, a1[3] * inv);
+      *reinterpret_cast<uint4*>(dst + 32 * c + 8 * grp) = w;
+    }
+    if (grp == 0 && p.lse != nullptr) p.lse[int64_t(token) * p.hq + head] = lse_v;
+  }
+}
+
+inline bool pf_al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+}  // namespace aspire
+
+extern "C" int aspire_prefill_block_tokens(int32_t num_qo_heads, int32_t num_kv_heads) {
+  using namespace aspire;
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads != 0) return 0;
+  const int G = num_qo_heads / num_kv_heads;
+  if (G > kPfRows || kPfRows % G != 0) return 0;
+  return kPfBlockRows / G;
+}
+
+extern "C" int aspire_prefill_run(const aspire_prefill_args* a, void* stream) {
+  using namespace aspire;
+  ASPIRE_CHECK_ARG(a != nullptr, "null argument");
+  ASPIRE_CHECK_ARG(a->head_dim == kHeadDim && a->page_size == kPage, "head_dim 128 and page_size 16 only");
+  const int bt = aspire_prefill_block_tokens(a->num_qo_heads, a->num_kv_heads);
+  ASPIRE_CHECK_ARG(bt > 0 && int64_t(a->total_blocks) * a->num_kv_heads < (int64_t(1) << 31),
+                   "num_qo_heads must be a multiple of num_kv_heads with a group dividing a wave's query rows "
+                   "(aspire_prefill_block_tokens > 0), and query blocks x kv heads below 2^31");
+  ASPIRE_CHECK_ARG(a->block_tokens == bt, "block_tokens must be aspire_prefill_block_tokens(hq, hkv)");
+  ASPIRE_CHECK_ARG(a->num_rows >= 0 && a->total_blocks >= 0, "bad sizes");
+  ASPIRE_CHECK_ARG(a->cache_stride_t > 0 && a->cache_stride_t < (int64_t(1) << 26),
+                   "cache_stride_t must be positive and below 2^26 elements (a page's rows span 32-bit offsets)");
+  if (a->num_rows == 0 || a->total_blocks == 0) return ASPIRE_OK;
+  ASPIRE_CHECK_ARG(a->q && a->kv_cache && a->kv_indices && a->kv_indptr && a->kv_last_page_len && a->qo_indptr &&
+                       a->block_indptr && a->out,
+                   "null pointer");
+  ASPIRE_CHECK_ARG(pf_al16(a->q) && pf_al16(a->kv_cache) && pf_al16(a->out), "q, kv_cache and out must be 16-byte aligned");
+  ASPIRE_CHECK_ARG(a->q_stride_t % 8 == 0 && a->q_stride_h % 8 == 0 && a->out_stride_t % 8 == 0 &&
+                       a->out_stride_h % 8 == 0 && a->cache_stride_p % 8 == 0 && a->cache_stride_kv % 8 == 0 &&
+                       a->cache_stride_t % 8 == 0 && a->cache_stride_h % 8 == 0,
+                   "strides must be multiples of 8 elements");
+  PrefillParams p;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.q_st = a->q_stride_t;
+  p.q_sh = a->q_stride_h;
+  p.cache = static_cast<const uint16_t*>(a->kv_cache);
+  p.c_sp = a->cache_stride_p;
+  p.c_skv = a->cache_stride_kv;
+  p.c_st = a->cache_stride_t;
+  p.c_sh = a->cache_stride_h;
+  p.kv_indices = a->kv_indices;
+  p.kv_indptr = a->kv_indptr;
+  p.last_page_len = a->kv_last_page_len;
+  p.qo_indptr = a->qo_indptr;
+  p.block_indptr = a->block_indptr;
+  p.num_rows = a->num_rows;
+  p.total_blocks = a->total_blocks;
+  p.block_tokens = bt;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.o_st = a->out_stride_t;
+  p.o_sh = a->out_stride_h;
+  p.lse = a->lse;
+  p.hq = a->num_qo_heads;
+  p.group = a->num_qo_heads / a->num_kv_heads;
+  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p.causal = a->causal;
+  hipLaunchKernelGGL(prefill_kernel, dim3(a->total_blocks * a->num_kv_heads), dim3(kPfThreads), 0,
+                     static_cast<hipStream_t>(stream), p);
+  ASPIRE_CHECK_LAUNCH();
+  return ASPIRE_OK;
+}

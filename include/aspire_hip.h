@@ -438,6 +438,37 @@ int aspire_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int6
 int aspire_argmax_rows(const void* logits, int64_t stride, int32_t rows, int32_t vocab, int64_t* ids,
                        void* stream);
 
+/* ------------------------------------------------------ (f3) prefill
+ * Chunked-prefill paged attention: replaces the attention FlashInfer's
+ * BatchPrefillWithPagedKVCacheWrapper runs for prompt chunks
+ * (aspire/models/sparse_draft_runner.py:199-209; the chunk loop of encode_slots,
+ * aspire/backends/base.py:1559-1674). Row b's queries [qo_indptr[b], qo_indptr[b+1])
+ * attend the first kv_len_b tokens of its pages kv_indices[kv_indptr[b] ..
+ * kv_indptr[b+1]) (kv_len_b = max(pages - 1, 0) * 16 + kv_last_page_len[b]), bottom-right
+ * causal when causal != 0; out and the base-2 lse as aspire_attention_run writes them.
+ * Work is split into query blocks of block_tokens tokens per (row, kv head):
+ * block_indptr[b] = sum over rows c < b of ceil(q_len_c / block_tokens), total_blocks =
+ * block_indptr[num_rows]; all index arrays are device arrays. No workspace. */
+typedef struct aspire_prefill_args {
+  const void* q; int64_t q_stride_t; int64_t q_stride_h;
+  const void* kv_cache; int64_t cache_stride_p; int64_t cache_stride_kv;
+  int64_t cache_stride_t; int64_t cache_stride_h;
+  const int32_t* kv_indices; const int32_t* kv_indptr; const int32_t* kv_last_page_len;
+  const int32_t* qo_indptr; const int32_t* block_indptr;
+  int32_t num_rows; int32_t total_blocks; int32_t block_tokens;
+  void* out; int64_t out_stride_t; int64_t out_stride_h;
+  float* lse;                      /* [T, H_q] or NULL */
+  int32_t num_qo_heads; int32_t num_kv_heads; int32_t head_dim; int32_t page_size;
+  float sm_scale; int32_t causal;
+} aspire_prefill_args;
+
+/* Tokens per query block for a head configuration: the workgroup's query rows (128 in
+ * the default build: 8 waves x 16) / (num_qo_heads / num_kv_heads), or 0 when the GQA
+ * group does not divide a wave's query rows (16 in the default build). Host only. */
+int aspire_prefill_block_tokens(int32_t num_qo_heads, int32_t num_kv_heads);
+
+int aspire_prefill_run(const aspire_prefill_args* args, void* stream);
+
 /* ------------------------------------------------------ (f4) sampling
  * Token sampling and speculative verification. One workgroup per row or request; the
  * uniforms of every draw are explicit device inputs (the Python layer draws them with

@@ -12,14 +12,16 @@ from oracle.attention import paged_attention
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("kernel", ["prefill", "decode"])
 @pytest.mark.parametrize("causal", [True, False])
-def test_chunked_prefill_matches_oracle(gpu, causal):
+def test_chunked_prefill_matches_oracle(gpu, causal, kernel):
     """Prompt chunks over cached prefixes (as encode_slots plans them): 300 new tokens over 700 cached,
-    a 1000-token first chunk, 64 over 4000, and a decode row, Qwen3-8B heads (GQA 4)."""
-    say("prefill", causal)
+    a 1000-token first chunk, 64 over 4000, and a decode row, Qwen3-8B heads (GQA 4); through the
+    dedicated prefill kernel and through the decode kernel's query tiles."""
+    say("prefill", causal, kernel)
     step = build_step(hq=32, hkv=8, ctx_len=[1000, 1000, 4064, 5000], q_len=[300, 1000, 64, 1],
                       is_draft=[0, 0, 0, 0], draft_budget=0, seed=31, device=gpu)
-    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD")
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD", kernel=kernel)
     w.plan(qo_indptr=step.qo_indptr, paged_kv_indptr=step.kv_indptr, paged_kv_indices=step.kv_indices,
            paged_kv_last_page_len=step.last_page_len, num_qo_heads=32, num_kv_heads=8, head_dim_qk=128,
            page_size=PAGE, q_data_type=torch.bfloat16, causal=causal)
@@ -42,3 +44,31 @@ def test_dump_refuses_split_rows(gpu):
     dump = torch.zeros(16 * 2 * 256, dtype=torch.float16, device=gpu)
     with pytest.raises(ValueError, match="whole rows"):
         w.run(step.q, step.cache, dump, 16, 256)
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (8, 8), (64, 8)])
+def test_prefill_kernel_head_groups_and_edges(gpu, hq, hkv):
+    """GQA groups 4, 2, 1 and 8 (query blocks of 64, 128, 256 and 32 tokens), rows that end mid-block
+    and mid-page, a row whose chunk starts at position 0, one with a single new token, and a tail page
+    with one valid key; stale slots past each row's length hold NaN keys and +inf values."""
+    say("prefill kernel edges", hq, hkv)
+    step = build_step(hq=hq, hkv=hkv, ctx_len=[257, 3001, 130, 16 * 40 + 1, 77], q_len=[257, 333, 1, 129, 20],
+                      is_draft=[0] * 5, draft_budget=0, seed=32, device=gpu)
+    cache = step.cache.clone()
+    table = step.block_table.cpu().numpy()
+    for b, n in enumerate(step.ctx_len):
+        last = (int(n) - 1) % PAGE + 1
+        if last < PAGE:
+            page = int(table[b, (int(n) - 1) // PAGE])
+            cache[page, 0, last:] = float("nan")
+            cache[page, 1, last:] = float("inf")
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD")
+    w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, hq, hkv, 128, PAGE, causal=True)
+    assert w._pf is not None
+    out, lse = w.run(step.q, cache, return_lse=True)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host,
+                                       step.kv_indices.cpu(), step.kv_len_host, num_kv_heads=hkv, causal=True)
+    T = step.total_tokens
+    attn_close(out[:T], ref_out[:T])
+    assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
