@@ -542,20 +542,25 @@ def measure_components(step, w, out, steps, plan_us):
                           ("4x2048_over_6144", [8192] * 4, [2048] * 4)):
         st = _build(hq=32, hkv=8, ctx_len=ctx, q_len=ql, is_draft=[0] * len(ctx), draft_budget=0, seed=4,
                     device=dev)
-        pw = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=dev), "NHD")
-        pw.plan(st.qo_indptr, st.kv_indptr, st.kv_indices, st.last_page_len, 32, 8, 128, PAGE, causal=True)
         po = torch.empty_like(st.q)
-        run = lambda: pw.run(st.q, st.cache, out=po)
-        for _ in range(3):
-            run()
-        us = timed(run, min(steps, 20), stream) * 1e3
+        times = {}
+        for kernel in ("prefill", "decode"):
+            pw = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=dev), "NHD", kernel=kernel)
+            pw.plan(st.qo_indptr, st.kv_indptr, st.kv_indices, st.last_page_len, 32, 8, 128, PAGE, causal=True)
+            run = lambda: pw.run(st.q, st.cache, out=po)
+            for _ in range(3):
+                run()
+            times[kernel] = timed(run, min(steps, 20), stream) * 1e3
+            del pw
+        us = times["prefill"]
         # causal FLOPs: QK and PV, 2 flops per MAC, each token against its visible keys
         keys = sum(sum(c - q + t + 1 for t in range(q)) for c, q in zip(ctx, ql))
         flops = 4 * 128 * 32 * keys
         pre[name] = {"us": round(us, 1), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
                      "frac_of_bf16_mfma_peak": round(flops / (us * 1e-6) / 2.5e15, 4),
-                     "split_rows": pw.plan_info.split_rows}
-        del st, pw, po
+                     "kernel": "prefill_kernel (aspire_prefill_run)",
+                     "decode_kernel_us": round(times["decode"], 1)}
+        del st, po
     res["prefill"] = pre
 
     # refresh layer (config 2): full attention + key-mean page scores + top-128 per (row, kv head)
