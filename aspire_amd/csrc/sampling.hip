@@ -1,11 +1,13 @@
 // (f4) Token sampling and speculative verification for gfx950.
 //
 // * topk_candidates_kernel: the top_k logits of a row and their ids, descending, ties to the
-//   lower id. Radix select on 16-bit order-preserving keys of the bf16 logits: a histogram of
-//   the high byte, then of the low byte among the boundary bin, gives the k-th key exactly;
-//   one ordered pass collects every larger key and the lowest-id ties; a bitonic sort in LDS
-//   orders the <= 1024 candidates. Histograms use 64 LDS sub-histograms (wave w, lane % 16)
-//   so lanes with equal keys rarely serialise on one counter.
+//   lower id. One 1024-thread workgroup per row, 16-byte loads. Radix select on 16-bit
+//   order-preserving keys of the bf16 logits: a histogram of the high byte, then of the low
+//   byte among the boundary bin, gives the k-th key exactly; one pass collects every key at or
+//   above it and a bitonic sort in LDS orders them (ties by id), so the first top_k are the
+//   answer. When the boundary key repeats so often that the candidates overflow LDS, an
+//   ordered pass ranks its ties by id instead. Histograms use 64 LDS sub-histograms
+//   (wave, lane % 4) so lanes with equal keys rarely serialise on one counter.
 // * logits_pipe_kernel: temperature, softmax and top-p renormalisation of one row in LDS.
 // * sample_kernel / chain_kernel / verify_kernel: inverse-CDF draws with the uniforms given
 //   (a contiguous chunk per thread, chunk sums scanned in thread order, so the prefix sums
@@ -160,29 +162,60 @@ struct TopKParams {
   int64_t* ids;      // [rows, k]
 };
 
-__global__ __launch_bounds__(kThreads) void topk_candidates_kernel(TopKParams p) {
-  __shared__ uint32_t hist[kSubHists][256];
+constexpr int kTkThreads = 1024;                 // one workgroup of 16 waves per row
+constexpr int kTkSubHists = (kTkThreads / 64) * 4;  // sub-histograms: (wave, lane % 4)
+constexpr int kTkCandCap = 2048;                  // candidates sorted in LDS
+
+template <bool kVec>
+__global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams p) {
+  __shared__ uint32_t hist[kTkSubHists][256];
   __shared__ uint32_t bins[256];
-  __shared__ uint64_t cand[kMaxTopK];
-  __shared__ int32_t sel[4];  // threshold key, count above, ties needed, candidates written
-  __shared__ int32_t tie_scan[kThreads];
+  __shared__ uint64_t cand[kTkCandCap];
+  __shared__ int32_t sel[5];  // threshold key, count above, ties needed, candidates written, ties present
+  __shared__ int32_t tie_scan[kTkThreads];
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int sub = (t >> 6) * 16 + (lane & 15);
+  const int sub = (t >> 6) * 4 + (lane & 3);
   const uint16_t* row = p.logits + int64_t(blockIdx.x) * p.stride;
   const int V = p.vocab;
   const int kk = min(p.k, V);
 
+  // f(i, key) over the row: 16-byte loads (8 logits) when rows are 16-byte aligned
+  auto for_each = [&](auto&& f) {
+    if constexpr (kVec) {
+      const int nv = V >> 3;
+      const uint4* rv = reinterpret_cast<const uint4*>(row);
+      for (int v = t; v < nv; v += kTkThreads) {
+        const uint4 w = rv[v];
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f(8 * v + 2 * e, bf16_key(uint16_t(u[e] & 0xffffu)));
+          f(8 * v + 2 * e + 1, bf16_key(uint16_t(u[e] >> 16)));
+        }
+      }
+      for (int i = (nv << 3) + t; i < V; i += kTkThreads) f(i, bf16_key(row[i]));
+    } else {
+      for (int i = t; i < V; i += kTkThreads) f(i, bf16_key(row[i]));
+    }
+  };
+  auto clear_hist = [&]() {
+    for (int i = t; i < kTkSubHists * 256; i += kTkThreads) (&hist[0][0])[i] = 0;
+  };
+  auto sum_hist = [&]() {
+    if (t < 256) {
+      uint32_t c = 0;
+      for (int h = 0; h < kTkSubHists; ++h) c += hist[h][t];
+      bins[t] = c;
+    }
+  };
+
   // pass 1: high byte
-  for (int i = t; i < kSubHists * 256; i += kThreads) (&hist[0][0])[i] = 0;
+  clear_hist();
   __syncthreads();
-  for (int i = t; i < V; i += kThreads) atomicAdd(&hist[sub][bf16_key(row[i]) >> 8], 1u);
+  for_each([&](int, uint32_t key) { atomicAdd(&hist[sub][key >> 8], 1u); });
   __syncthreads();
-  {
-    uint32_t c = 0;
-    for (int h = 0; h < kSubHists; ++h) c += hist[h][t];
-    bins[t] = c;
-  }
+  sum_hist();
   __syncthreads();
   if (t == 0) {
     uint32_t above = 0;
@@ -197,18 +230,13 @@ __global__ __launch_bounds__(kThreads) void topk_candidates_kernel(TopKParams p)
   __syncthreads();
   const uint32_t hb = uint32_t(sel[0]);
   // pass 2: low byte among keys in the boundary bin
-  for (int i = t; i < kSubHists * 256; i += kThreads) (&hist[0][0])[i] = 0;
+  clear_hist();
   __syncthreads();
-  for (int i = t; i < V; i += kThreads) {
-    const uint32_t key = bf16_key(row[i]);
+  for_each([&](int, uint32_t key) {
     if ((key >> 8) == hb) atomicAdd(&hist[sub][key & 255], 1u);
-  }
+  });
   __syncthreads();
-  {
-    uint32_t c = 0;
-    for (int h = 0; h < kSubHists; ++h) c += hist[h][t];
-    bins[t] = c;
-  }
+  sum_hist();
   __syncthreads();
   if (t == 0) {
     uint32_t above = uint32_t(sel[1]);
@@ -221,46 +249,59 @@ __global__ __launch_bounds__(kThreads) void topk_candidates_kernel(TopKParams p)
     sel[1] = int(above);                      // keys above it
     sel[2] = kk - int(above);                 // ties to take, lowest ids first
     sel[3] = 0;
+    sel[4] = int(bins[lb]);                   // keys equal to it
   }
   __syncthreads();
   const uint32_t kth = uint32_t(sel[0]);
   const int ties = sel[2];
-  // pass 3: contiguous chunk per thread so tie ranks follow the id order
-  const int chunk = (V + kThreads - 1) / kThreads;
-  const int i0 = min(t * chunk, V), i1 = min(i0 + chunk, V);
-  int my_ties = 0;
-  for (int i = i0; i < i1; ++i) my_ties += bf16_key(row[i]) == kth;
-  tie_scan[t] = my_ties;
-  __syncthreads();
-  if (t == 0) {
-    int acc = 0;
-    for (int j = 0; j < kThreads; ++j) {
-      const int c = tie_scan[j];
-      tie_scan[j] = acc;
-      acc += c;
+  // sort key: larger key first, then the lower id
+  auto push = [&](int i, uint32_t key) {
+    const int slot = atomicAdd(&sel[3], 1);
+    cand[slot] = (uint64_t(key) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+  };
+  int n_sort;
+  if (sel[1] + sel[4] <= kTkCandCap) {
+    // pass 3: every key >= the k-th; sorting puts the lowest-id ties first
+    for_each([&](int i, uint32_t key) {
+      if (key >= kth) push(i, key);
+    });
+    n_sort = sel[1] + sel[4];
+  } else {
+    // many equal keys at the boundary: rank the ties in id order (a contiguous chunk per
+    // thread, chunk counts scanned in thread order) and take only the first ones
+    const int chunk = (V + kTkThreads - 1) / kTkThreads;
+    const int i0 = min(t * chunk, V), i1 = min(i0 + chunk, V);
+    int my_ties = 0;
+    for (int i = i0; i < i1; ++i) my_ties += bf16_key(row[i]) == kth;
+    tie_scan[t] = my_ties;
+    __syncthreads();
+    if (t == 0) {
+      int acc = 0;
+      for (int j = 0; j < kTkThreads; ++j) {
+        const int c = tie_scan[j];
+        tie_scan[j] = acc;
+        acc += c;
+      }
     }
-  }
-  __syncthreads();
-  int tie_rank = tie_scan[t];
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = bf16_key(row[i]);
-    bool take = key > kth;
-    if (key == kth) take = tie_rank++ < ties;
-    if (take) {
-      const int slot = atomicAdd(&sel[3], 1);
-      // sort key: larger key first, then the lower id
-      cand[slot] = (uint64_t(key) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+    __syncthreads();
+    int tie_rank = tie_scan[t];
+    for (int i = i0; i < i1; ++i) {
+      const uint32_t key = bf16_key(row[i]);
+      bool take = key > kth;
+      if (key == kth) take = tie_rank++ < ties;
+      if (take) push(i, key);
     }
+    n_sort = kk;
   }
   __syncthreads();
   int n2 = 1;
-  while (n2 < kk) n2 <<= 1;
-  for (int i = kk + t; i < n2; i += kThreads) cand[i] = 0;
+  while (n2 < n_sort) n2 <<= 1;
+  for (int i = n_sort + t; i < n2; i += kTkThreads) cand[i] = 0;
   __syncthreads();
   // bitonic sort, descending
   for (int size = 2; size <= n2; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = t; i < n2; i += kThreads) {
+      for (int i = t; i < n2; i += kTkThreads) {
         const int j = i ^ stride;
         if (j > i) {
           const bool desc = (i & size) == 0;
@@ -276,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void topk_candidates_kernel(TopKParams p)
   }
   uint16_t* vout = p.values + int64_t(blockIdx.x) * p.k;
   int64_t* iout = p.ids + int64_t(blockIdx.x) * p.k;
-  for (int j = t; j < p.k; j += kThreads) {
+  for (int j = t; j < p.k; j += kTkThreads) {
     if (j < kk) {
       const uint32_t id = 0xffffffffu - uint32_t(cand[j] & 0xffffffffu);
       vout[j] = row[id];  // the logit's own bits (a -0 stays -0)
@@ -547,7 +588,11 @@ extern "C" int aspire_topk_candidates(const void* logits, int64_t stride, int32_
   ASPIRE_CHECK_ARG(logits && values && ids, "null pointer");
   TopKParams p{static_cast<const uint16_t*>(logits), stride, vocab, top_k, vocab_start,
                static_cast<uint16_t*>(values), ids};
-  hipLaunchKernelGGL(topk_candidates_kernel, dim3(rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+  const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && stride % 8 == 0;
+  if (vec)
+    hipLaunchKernelGGL(topk_candidates_kernel<true>, dim3(rows), dim3(kTkThreads), 0, static_cast<hipStream_t>(stream), p);
+  else
+    hipLaunchKernelGGL(topk_candidates_kernel<false>, dim3(rows), dim3(kTkThreads), 0, static_cast<hipStream_t>(stream), p);
   ASPIRE_CHECK_LAUNCH();
   return ASPIRE_OK;
 }

@@ -33,6 +33,36 @@ def test_topk_candidates_exact(gpu, rows, vocab, k, start):
     assert torch.equal(vals.cpu().view(torch.int16), ref_v.view(torch.int16))
 
 
+@pytest.mark.parametrize("case", ["continuous", "all_equal", "misaligned", "equal_blocks"])
+def test_topk_candidates_paths(gpu, case):
+    """Both collection paths and both load widths: continuous logits (few ties: one pass over every
+    key >= the k-th), rows of one repeated value and rows where the boundary value repeats
+    thousands of times (ties overflow the candidate buffer: the id-ordered tie ranking), and a
+    view whose rows start 2 bytes past a 16-byte boundary (2-byte loads)."""
+    say("topk candidates path", case)
+    g = torch.Generator().manual_seed(11)
+    rows, vocab, k = 6, 20016, 100
+    if case == "continuous":
+        logits = torch.randn(rows, vocab, generator=g).to(torch.bfloat16)
+    elif case == "all_equal":
+        logits = torch.full((rows, vocab), 0.5).to(torch.bfloat16)
+        logits[1] = -3.0
+    elif case == "misaligned":
+        logits = (torch.randn(rows, vocab, generator=g) * 3).round().to(torch.bfloat16)
+    else:
+        logits = torch.zeros(rows, vocab).to(torch.bfloat16)
+        logits[:, ::7] = 1.0                       # ~2,860 keys tie at the boundary value
+        logits[:, 5:40] = 2.0                      # 35 strictly above it
+    x = logits.to(gpu) if case != "misaligned" else torch.cat(
+        [torch.zeros(rows, 1, dtype=torch.bfloat16), logits], 1).to(gpu)[:, 1:]
+    assert (x.data_ptr() % 16 != 0) == (case == "misaligned")
+    vals, ids = local_topk_candidates(x, k)
+    torch.cuda.synchronize()
+    ref_v, ref_i = osamp.topk_candidates(logits, k)
+    assert torch.equal(ids.cpu(), ref_i)
+    assert torch.equal(vals.cpu().view(torch.int16), ref_v.view(torch.int16))
+
+
 def test_merge_topk_candidates(gpu):
     g = torch.Generator().manual_seed(3)
     vals = (torch.randn(6, 4 * 50, generator=g) * 2).round().to(torch.bfloat16)
