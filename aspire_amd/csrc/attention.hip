@@ -123,11 +123,13 @@ constexpr int kLdsChunks = kStageChunks + (ASPIRE_DIRECT_VT_MIN_NT <= kMaxRowTil
 #define ASPIRE_DIRECT_VT_EARLY_V 0
 #endif
 
-// LDS row swizzle: 16-byte chunk c of key row r is stored at chunk c ^ swz(r). swz swaps
-// the two 2-bit halves of r, which keeps all three access patterns on distinct banks:
-// whole-row writes (one row, 64 consecutive chunks), the 16-row column reads of the MFMA
-// operand layout (rows 0..15, chunk 4c + grp) and the transpose reads of V^T (rows
-// 4grp + 0..3, chunks 4m + 0..3): (4m + k) ^ swz(4grp + q) = 4(m ^ q) + (k ^ grp).
+// LDS row swizzle: 16-byte chunk c of key row r is stored at chunk c ^ swz(r); swz swaps
+// the two 2-bit halves of r. Whole-row writes (one row, 64 consecutive chunks) are
+// conflict-free; the 16-row column reads of the MFMA operand layout (rows 0..15, chunk
+// 4c + grp) and the transpose reads of V^T (rows 4grp + 0..3) measure pairwise bank
+// conflicts on gfx950 (8 and 4 cycles per read where 4 and 2 are possible). Placements that
+// remove them (c ^ r for column reads; c ^ swz(r) with the 8-byte halves swapped on rows
+// with bit 2 set for transpose reads) measured no faster here: this kernel is HBM-bound.
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | (r >> 2); }
 
 // LDS-only release/acquire around the workgroup barrier: waits for this
@@ -541,8 +543,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       // LDS; after a barrier every wave reads its own head's rows from LDS in the
       // MFMA operand layout. Contiguous 1 KiB loads stream measurably faster
       // from HBM than 16 rows x 64 B per instruction. LDS chunk c of key row r
-      // sits at c ^ swz(r), so row writes, column reads and transpose reads are all
-      // free of bank conflicts. Two LDS buffers: page pg is read from one while
+      // sits at c ^ swz(r) (see swz). Two LDS buffers: page pg is read from one while
       // page pg + 1 is stored to the other and page pg + 2 is in flight.
       if (pb < pe) {
         const int wl = (threadIdx.x >> 6) & 3;
