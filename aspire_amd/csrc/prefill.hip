@@ -85,7 +85,10 @@ struct PrefillParams {
 
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfWavesPerEu))) void prefill_kernel(
     PrefillParams p) {
-  __shared__ uint4 stage[2 * kPfStage];
+  __shared__ uint4 stg0[kPfStage];
+  __shared__ uint4 stg1[kPfStage];
+  __shared__ uint4 stg2[kPfStage];
+  __shared__ uint4 stg3[kPfStage];
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(threadIdx.x >> 6);
   const int r = lane & 15, grp = lane >> 4;
@@ -159,56 +162,58 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   }
 
   // Staging. A step's 1024 chunks (16 B) are 4 kinds of 256: page 2s K rows, its V rows, page
-  // 2s + 1 K rows, V rows. Thread t moves chunks t + i * threads; a chunk's kind is uniform
-  // across each wave, so its source is one scalar buffer descriptor per (kind, page) and a
-  // fixed per-lane offset. Loads go through buffer descriptors: a chunk past vlim (stale slots
-  // past kv_len, pages the block does not reach) gets an offset beyond the descriptor's range
-  // and comes back as zeros, so the P.V loop needs no masks.
-  const int t = threadIdx.x;
-  const int crow = (t & 255) >> 4, ccol = t & 15;
-  const int voff = crow * int(p.c_st) * 2 + ccol * 16;
-  const int lds_off = (t & 255 & ~15) + (ccol ^ pf_swz(crow));
+  // 2s + 1 K rows, V rows. They travel from HBM straight into LDS (buffer_load ... lds): wave w's
+  // i-th load writes the stage's chunks w * 64 + i * threads + lane, one contiguous 1 KiB, so a
+  // kind is uniform across the wave (one scalar buffer descriptor per kind and page) and each
+  // lane fetches the global chunk that belongs at its LDS position. K rows are placed with chunk
+  // c of row r at c ^ r (conflict-free column reads), V rows at c ^ swz(r) (the transpose reads).
+  // A chunk past vlim (stale slots past kv_len, pages the block does not reach) is requested
+  // with an offset beyond the descriptor's range: the load then writes zeros into LDS.
+  const int crow = (wave & 3) * 4 + (lane >> 4), cpos = lane & 15;
+  const int voff_k = crow * int(p.c_st) * 2 + (cpos ^ crow) * 16;
+  const int voff_v = crow * int(p.c_st) * 2 + (cpos ^ pf_swz(crow)) * 16;
   const int span = wave_uniform(15 * int(p.c_st) * 2 + 256);
-  const __amdgpu_buffer_rsrc_t ids_rs = __builtin_amdgcn_make_buffer_rsrc(
-      uniform_ptr(p.kv_indices + list0), (short)0, np * 4, kPfBufferConfig);
-  // page ids through vector loads (in order with the K/V loads, so their wait is exact)
-  auto page_ids = [&](int st_idx, int& ia, int& ib) {
-    ia = __builtin_amdgcn_raw_buffer_load_b32(ids_rs, 8 * st_idx, 0, 0);
-    ib = __builtin_amdgcn_raw_buffer_load_b32(ids_rs, 8 * st_idx + 4, 0, 0);
-  };
-  constexpr int kPer = kPfStage / kPfThreads;  // chunks per thread
-  auto issue = [&](int k, int ia, int ib, uint4(&st)[kPer]) {
-    const int64_t pa = wave_uniform(ia), pb = wave_uniform(ib);
+  typedef const __attribute__((address_space(4))) int32_t* const_ids_t;
+  const const_ids_t ids = (const_ids_t)(p.kv_indices + list0);
+  auto page_id = [&](int pg) -> int { return ids[min(pg, max(np - 1, 0))]; };
+  constexpr int kPer = kPfStage / kPfThreads;  // 1 KiB loads per wave and step
+  auto issue = [&](uint4* buf, int k, int ia, int ib) {
     const bool edge = k * kPfStepKeys + kPfStepKeys > vlim;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int kind = (wave * 64 + i * kPfThreads) >> 8;
-      const int64_t phys = (kind >> 1) ? pb : pa;
+      const int base = wave * 64 + i * kPfThreads;  // first chunk of this load
+      const int kind = base >> 8;
+      const int64_t phys = (kind >> 1) ? ib : ia;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           uniform_ptr(p.cache + phys * p.c_sp + (kind & 1) * p.c_skv + int64_t(g) * p.c_sh), (short)0, span,
           kPfBufferConfig);
-      int off = voff;
-      if (edge) off = k * kPfStepKeys + (kind >> 1) * kPage + crow < vlim ? voff : kPfOutOfRange;
-      const u32x4p v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-      st[i] = make_uint4(v.x, v.y, v.z, v.w);
+      int off = (kind & 1) ? voff_v : voff_k;
+      if (edge) off = k * kPfStepKeys + (kind >> 1) * kPage + crow < vlim ? off : kPfOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(buf + base), 16, off,
+                                               0, 0, 0);
     }
   };
-  auto store = [&](int buf, const uint4(&st)[kPer]) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) stage[buf * kPfStage + ((wave * 64 + i * kPfThreads) >> 8) * kPfHalf + lds_off] = st[i];
+  // LDS release / acquire around the barrier without a memory fence: the fence would also wait
+  // for the step loads in flight (they write LDS). The explicit wait covers this wave's loads of
+  // the next step (2 * kPer later ones may stay in flight) and its LDS reads of this step's
+  // buffer, which the loads issued after the barrier overwrite; the empty asm statements keep
+  // the compiler from moving LDS accesses across the barrier.
+  auto step_barrier = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0070 | (2 * kPer));  // vmcnt(2 * kPer), lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
 
   const int vt_row = 4 * grp + (r >> 2);
-  auto compute = [&](int s) {
-    const int buf = s & 1;
+  auto compute = [&](const uint4* kb, int s) {
     const int key0 = s * kPfStepKeys;
     // S^T of both pages: lane (r, grp) holds keys key0 + 4grp + i (sa) and key0 + 16 + 4grp + i (sb)
-    const uint4* kb = stage + buf * kPfStage;
     f32x4 sa[kPfTiles], sb[kPfTiles];
     {
       uint4 kr[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kr[c] = kb[r * kPfRowChunks + ((4 * c + grp) ^ pf_swz(r))];
+      for (int c = 0; c < 4; ++c) kr[c] = kb[r * kPfRowChunks + ((4 * c + grp) ^ r)];
 #pragma unroll
       for (int tt = 0; tt < kPfTiles; ++tt) {
         sa[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
         for (int c = 0; c < 4; ++c) sa[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sa[tt]);
       }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kr[c] = kb[kPfPage + r * kPfRowChunks + ((4 * c + grp) ^ pf_swz(r))];
+      for (int c = 0; c < 4; ++c) kr[c] = kb[kPfPage + r * kPfRowChunks + ((4 * c + grp) ^ r)];
 #pragma unroll
       for (int tt = 0; tt < kPfTiles; ++tt) {
         sb[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -272,7 +277,9 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
         for (int j = 0; j < 8; ++j) acc[tt][j] *= alpha[tt];
     }
     // O^T += V^T . P^T with 16x16x32 MFMAs over the step's 32 keys: lane (r, grp) carries keys
-    // 4grp..4grp+3 of both pages, the order P^T's fragment uses; V^T by transpose reads
+    // 4grp..4grp+3 of both pages, the order P^T's fragment uses; V^T by transpose reads. Keys
+    // from vlim on were requested out of range, which writes zeros into LDS, so 0 * stale never
+    // reaches the sums.
     const char* va = reinterpret_cast<const char*>(kb + kPfHalf + vt_row * kPfRowChunks);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -287,35 +294,36 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
     }
   };
 
-  // Pipeline: step s computes from LDS buffer s & 1; its K/V were loaded into registers at the
-  // start of step s - 2 (two steps to land) and stored at the end of step s - 1. The page ids
-  // of step s + 3 are loaded at the start of step s, ahead of that step's K/V loads.
-  // Every step issues the same loads (steps past the block read as zeros through the
-  // out-of-range offset), so the outstanding-load queue has one shape on every iteration:
-  // [ids(s + 2), K/V(s + 1)] at the top of step s.
+  // Pipeline over four LDS stage buffers (step k in buffer k % 4, four separate LDS objects so
+  // the compiler can tell a load into one from a read of another): at the start of step s the
+  // loads of step s + 3 go into the buffer step s - 1 used (free since that step's barrier);
+  // the barrier at the end of step s waits for step s + 1's loads. Each load thus has three
+  // steps to land. Page ids are scalar loads one step ahead of their use. Every step issues
+  // the same loads (steps past the block read nothing: every chunk is out of range), so the
+  // wait count is the same on every iteration.
   if (steps > 0) {
-    uint4 st0[kPer], st1[kPer];
-    int i0a, i0b, i1a, i1b, na, nb;
-    page_ids(0, i0a, i0b);
-    page_ids(1, i1a, i1b);
-    issue(0, i0a, i0b, st0);
-    page_ids(2, na, nb);
-    issue(1, i1a, i1b, st1);
-    store(0, st0);
-    __syncthreads();
-    auto body = [&](int s, uint4(&st_issue)[kPer], uint4(&st_store)[kPer]) {
+    int a0 = page_id(0), b0 = page_id(1), a1 = page_id(2), b1 = page_id(3), a2 = page_id(4), b2 = page_id(5);
+    issue(stg0, 0, a0, b0);
+    issue(stg1, 1, a1, b1);
+    issue(stg2, 2, a2, b2);
+    int na = page_id(6), nb = page_id(7);
+    __builtin_amdgcn_s_waitcnt(0x0070 | (2 * kPer));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    auto body = [&](int s, uint4* cur, uint4* fill) {
       const int ca = na, cb = nb;
-      page_ids(s + 3, na, nb);
-      issue(s + 2, ca, cb, st_issue);
-      if (s < steps && s * kPfStepKeys <= w_last) compute(s);
-      if (s + 1 < steps) store((s + 1) & 1, st_store);
-      __syncthreads();
+      na = page_id(2 * (s + 4));
+      nb = page_id(2 * (s + 4) + 1);
+      issue(fill, s + 3, ca, cb);
+      if (s < steps && s * kPfStepKeys <= w_last) compute(cur, s);
+      step_barrier();
     };
-    // two steps per trip, the second one possibly past the block (loads of zeros, no compute,
-    // no store): both halves keep one shape, so the loads in flight never force a wait early
-    for (int s = 0; s < steps; s += 2) {
-      body(s, st0, st1);
-      body(s + 1, st1, st0);
+    for (int s = 0; s < steps; s += 4) {
+      body(s, stg0, stg3);
+      body(s + 1, stg1, stg0);
+      body(s + 2, stg2, stg1);
+      body(s + 3, stg3, stg2);
     }
   }
 
