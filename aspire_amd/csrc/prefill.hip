@@ -2,14 +2,16 @@
 //
 // A workgroup of kPfWaves waves takes one query block of one (row, kv head): kPfWaves x 16 x
 // kPfTiles query rows (block_tokens = that / G tokens, G = q heads per kv head), 16 x kPfTiles
-// rows per wave. Every page of the block's keys is read from HBM once per workgroup: the
-// waves load two pages at a time (K and V rows of this kv head, 16 KiB) into a
-// double-buffered LDS stage and each wave then runs its tiles over those 32 keys:
-//   * S^T = K . Q^T per page and tile with 4 v_mfma_f32_16x16x32_bf16 (K rows from LDS in
-//     the swizzled layout, Q fragments in registers); lane (r, grp) holds S^T[key 4grp + i][row r];
+// rows per wave. Every page of the block's keys is read from HBM once per workgroup: two pages
+// at a time (K and V rows of this kv head, 16 KiB) go straight from HBM into one of four LDS
+// stage buffers (buffer_load ... lds, three steps ahead), and each wave runs its tiles over
+// those 32 keys:
+//   * S^T = K . Q^T per page and tile with 4 v_mfma_f32_16x16x32_bf16 (K rows from LDS,
+//     Q fragments in registers); lane (r, grp) holds S^T[key 4grp + i][row r];
 //   * online softmax in fp32 over the 32 keys (exp2 with the scale folded into its argument,
 //     base-2 LSE; row max across the 4 lane groups with permlane swaps), causal masking only
-//     on steps that reach a row's limit, accumulator rescale only when some row's max moved;
+//     on steps that reach a row's limit; the running max moves only when it grows by more
+//     than kPfSlack, so the accumulators are rescaled on few steps;
 //   * O^T += V^T . P^T with 8 v_mfma_f32_16x16x32_bf16 per tile: each lane's 8 keys are
 //     keys 4grp..4grp+3 of both pages (the order S^T left them in), V^T comes from LDS with
 //     transpose reads (ds_read_b64_tr_b16) and is shared by the wave's tiles.
@@ -24,11 +26,15 @@ namespace {
 
 constexpr float kNegInfP = -__builtin_huge_valf();
 #ifndef ASPIRE_PF_WAVES
-#define ASPIRE_PF_WAVES 8
+#define ASPIRE_PF_WAVES 16
 #endif
 #ifndef ASPIRE_PF_TILES
 #define ASPIRE_PF_TILES 1
 #endif
+#ifndef ASPIRE_PF_RESCALE_SLACK
+#define ASPIRE_PF_RESCALE_SLACK 8
+#endif
+constexpr float kPfSlack = ASPIRE_PF_RESCALE_SLACK;
 constexpr int kPfWaves = ASPIRE_PF_WAVES;   // waves per workgroup
 constexpr int kPfTiles = ASPIRE_PF_TILES;   // 16-row query tiles per wave
 constexpr int kPfRows = 16 * kPfTiles;      // query rows per wave
@@ -253,7 +259,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
       }
       float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
       mx = max_xor32(max_xor16(mx));
-      const float m_new = fmaxf(m[tt], mx * p.scale_log2);
+      // the running max moves only when it grows by more than kPfSlack (log2 units): the
+      // exponentials stay below 2^kPfSlack, and the accumulators are rescaled on few steps
+      const float m_cand = mx * p.scale_log2;
+      const float m_new = m_cand > m[tt] + kPfSlack ? m_cand : m[tt];
       const float m_use = m_new == kNegInfP ? 0.f : m_new;
       const float a = __builtin_amdgcn_exp2f(m[tt] - m_use);
       float pv[8];

@@ -26,7 +26,6 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxTopK = 1024;
 constexpr int kMaxPipeWidth = 4096;
-constexpr int kSubHists = kWaves * 16;
 
 // Order-preserving 16-bit key of a bf16 value; -0 and +0 share a key (they compare equal, so
 // they tie and fall back to the id order).

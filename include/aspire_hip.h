@@ -462,8 +462,8 @@ typedef struct aspire_prefill_args {
   float sm_scale; int32_t causal;
 } aspire_prefill_args;
 
-/* Tokens per query block for a head configuration: the workgroup's query rows (128 in
- * the default build: 8 waves x 16) / (num_qo_heads / num_kv_heads), or 0 when the GQA
+/* Tokens per query block for a head configuration: the workgroup's query rows (256 in
+ * the default build: 16 waves x 16) / (num_qo_heads / num_kv_heads), or 0 when the GQA
  * group does not divide a wave's query rows (16 in the default build). Host only. */
 int aspire_prefill_block_tokens(int32_t num_qo_heads, int32_t num_kv_heads);
 
