@@ -72,3 +72,41 @@ def test_prefill_kernel_head_groups_and_edges(gpu, hq, hkv):
     T = step.total_tokens
     attn_close(out[:T], ref_out[:T])
     assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
+
+
+def test_prefill_kernel_separate_kv_tensors_and_gqa16(gpu):
+    """K and V in two tensors (the (k_cache, v_cache) form, so the K-to-V distance is an
+    arbitrary allocation offset), and GQA 16 (16-token query blocks)."""
+    say("prefill kernel separate k/v, GQA 16")
+    step = build_step(hq=32, hkv=2, ctx_len=[700, 129, 40], q_len=[300, 129, 7], is_draft=[0] * 3, draft_budget=0,
+                      seed=33, device=gpu)
+    k_cache = step.cache[:, 0].contiguous()
+    v_cache = step.cache[:, 1].contiguous()
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD")
+    w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, 32, 2, 128, PAGE, causal=True)
+    assert w._pf is not None and w._pf["block_tokens"] * 16 == 256
+    out, lse = w.run(step.q, (k_cache, v_cache), return_lse=True)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host,
+                                       step.kv_indices.cpu(), step.kv_len_host, num_kv_heads=2, causal=True)
+    T = step.total_tokens
+    attn_close(out[:T], ref_out[:T])
+    assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_kernel_full_chunk_matches_decode_path(gpu, causal):
+    """The reference's largest prompt chunk (8,192 tokens, Qwen3-8B heads) at full size: the
+    dedicated kernel against the decode kernel's query tiles, which the tests above pin to the
+    oracle on the same rule (the CPU oracle at this size would take minutes)."""
+    say("prefill 8192 chunk vs decode path", causal)
+    step = build_step(hq=32, hkv=8, ctx_len=[8192], q_len=[8192], is_draft=[0], draft_budget=0, seed=34, device=gpu)
+    res = {}
+    for kernel in ("prefill", "decode"):
+        w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD", kernel=kernel)
+        w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, 32, 8, 128, PAGE, causal=causal)
+        res[kernel] = w.run(step.q, step.cache, return_lse=True)
+        torch.cuda.synchronize()
+    (out_p, lse_p), (out_d, lse_d) = res["prefill"], res["decode"]
+    attn_close(out_p, out_d)
+    assert (lse_p - lse_d).abs().max().item() < 2e-3
