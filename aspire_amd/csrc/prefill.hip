@@ -35,6 +35,11 @@ constexpr float kNegInfP = -__builtin_huge_valf();
 #define ASPIRE_PF_RESCALE_SLACK 8
 #endif
 constexpr float kPfSlack = ASPIRE_PF_RESCALE_SLACK;
+#ifndef ASPIRE_PF_STAGES
+#define ASPIRE_PF_STAGES 4
+#endif
+constexpr int kPfStages = ASPIRE_PF_STAGES;  // LDS stage buffers (loads run kPfStages - 1 steps ahead)
+static_assert(kPfStages >= 3 && kPfStages <= 8, "3 to 8 stage buffers");
 constexpr int kPfWaves = ASPIRE_PF_WAVES;   // waves per workgroup
 constexpr int kPfTiles = ASPIRE_PF_TILES;   // 16-row query tiles per wave
 constexpr int kPfRows = 16 * kPfTiles;      // query rows per wave
@@ -95,6 +100,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   __shared__ uint4 stg1[kPfStage];
   __shared__ uint4 stg2[kPfStage];
   __shared__ uint4 stg3[kPfStage];
+  __shared__ uint4 stg4[kPfStages > 4 ? kPfStage : 1];
+  __shared__ uint4 stg5[kPfStages > 5 ? kPfStage : 1];
+  __shared__ uint4 stg6[kPfStages > 6 ? kPfStage : 1];
+  __shared__ uint4 stg7[kPfStages > 7 ? kPfStage : 1];
+  uint4* const stages[8] = {stg0, stg1, stg2, stg3, stg4, stg5, stg6, stg7};
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(threadIdx.x >> 6);
   const int r = lane & 15, grp = lane >> 4;
@@ -183,6 +193,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   const const_ids_t ids = (const_ids_t)(p.kv_indices + list0);
   auto page_id = [&](int pg) -> int { return ids[min(pg, max(np - 1, 0))]; };
   constexpr int kPer = kPfStage / kPfThreads;  // 1 KiB loads per wave and step
+  // the barrier's wait: this wave's loads of the next step have landed, those of the
+  // kPfStages - 2 steps after it may still be in flight (s_waitcnt vmcnt(n) lgkmcnt(0), gfx9
+  // encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at 7, lgkmcnt 11:8)
+  constexpr int kPfWaitN = (kPfStages - 2) * kPer;
+  constexpr int kPfWait = (kPfWaitN & 15) | ((kPfWaitN >> 4) << 14) | 0x70;
   auto issue = [&](uint4* buf, int k, int ia, int ib) {
     const bool edge = k * kPfStepKeys + kPfStepKeys > vlim;
 #pragma unroll
@@ -205,7 +220,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   // buffer, which the loads issued after the barrier overwrite; the empty asm statements keep
   // the compiler from moving LDS accesses across the barrier.
   auto step_barrier = [&]() {
-    __builtin_amdgcn_s_waitcnt(0x0070 | (2 * kPer));  // vmcnt(2 * kPer), lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(kPfWait);  // vmcnt((kPfStages - 2) * kPer), lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -303,36 +318,32 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
     }
   };
 
-  // Pipeline over four LDS stage buffers (step k in buffer k % 4, four separate LDS objects so
-  // the compiler can tell a load into one from a read of another): at the start of step s the
-  // loads of step s + 3 go into the buffer step s - 1 used (free since that step's barrier);
-  // the barrier at the end of step s waits for step s + 1's loads. Each load thus has three
-  // steps to land. Page ids are scalar loads one step ahead of their use. Every step issues
-  // the same loads (steps past the block read nothing: every chunk is out of range), so the
-  // wait count is the same on every iteration.
+  // Pipeline over kPfStages LDS stage buffers (step k in buffer k % kPfStages, separate LDS
+  // objects so the compiler can tell a load into one from a read of another): at the start of
+  // step s the loads of step s + kPfStages - 1 go into the buffer step s - 1 used (free since
+  // that step's barrier); the barrier at the end of step s waits for step s + 1's loads. Page
+  // ids are scalar loads one step ahead of their use. Every step issues the same loads (steps
+  // past the block read nothing: every chunk is out of range), so the wait count is the same
+  // on every iteration.
   if (steps > 0) {
-    int a0 = page_id(0), b0 = page_id(1), a1 = page_id(2), b1 = page_id(3), a2 = page_id(4), b2 = page_id(5);
-    issue(stg0, 0, a0, b0);
-    issue(stg1, 1, a1, b1);
-    issue(stg2, 2, a2, b2);
-    int na = page_id(6), nb = page_id(7);
-    __builtin_amdgcn_s_waitcnt(0x0070 | (2 * kPer));
+#pragma unroll
+    for (int k = 0; k < kPfStages - 1; ++k) issue(stages[k], k, page_id(2 * k), page_id(2 * k + 1));
+    int na = page_id(2 * (kPfStages - 1)), nb = page_id(2 * (kPfStages - 1) + 1);
+    __builtin_amdgcn_s_waitcnt(kPfWait);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     auto body = [&](int s, uint4* cur, uint4* fill) {
       const int ca = na, cb = nb;
-      na = page_id(2 * (s + 4));
-      nb = page_id(2 * (s + 4) + 1);
-      issue(fill, s + 3, ca, cb);
+      na = page_id(2 * (s + kPfStages));
+      nb = page_id(2 * (s + kPfStages) + 1);
+      issue(fill, s + kPfStages - 1, ca, cb);
       if (s < steps && s * kPfStepKeys <= w_last) compute(cur, s);
       step_barrier();
     };
-    for (int s = 0; s < steps; s += 4) {
-      body(s, stg0, stg3);
-      body(s + 1, stg1, stg0);
-      body(s + 2, stg2, stg1);
-      body(s + 3, stg3, stg2);
+    for (int s = 0; s < steps; s += kPfStages) {
+#pragma unroll
+      for (int u = 0; u < kPfStages; ++u) body(s + u, stages[u], stages[(u + kPfStages - 1) % kPfStages]);
     }
   }
 
