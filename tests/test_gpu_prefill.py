@@ -110,3 +110,21 @@ def test_prefill_kernel_full_chunk_matches_decode_path(gpu, causal):
     (out_p, lse_p), (out_d, lse_d) = res["prefill"], res["decode"]
     attn_close(out_p, out_d)
     assert (lse_p - lse_d).abs().max().item() < 2e-3
+
+
+def test_prefill_head_group_outside_the_kernel_takes_the_decode_path(gpu):
+    """GQA 6 (24 query heads over 4 kv heads) does not divide the prefill kernel's 16-row
+    wave tile: plan() routes the rows to the mixed kernel's query tiles, same results."""
+    say("prefill GQA 6")
+    step = build_step(hq=24, hkv=4, ctx_len=[500, 90], q_len=[200, 90], is_draft=[0, 0], draft_budget=0, seed=35,
+                      device=gpu)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD")
+    w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, 24, 4, 128, PAGE, causal=True)
+    assert w._pf is None
+    out, lse = w.run(step.q, step.cache, return_lse=True)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host,
+                                       step.kv_indices.cpu(), step.kv_len_host, num_kv_heads=4, causal=True)
+    T = step.total_tokens
+    attn_close(out[:T], ref_out[:T])
+    assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
