@@ -167,11 +167,15 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
       limit[t] = -1;
     }
   }
-  float m[kPfTiles], l[kPfTiles];
+  // Per row (lane r of each tile): the running max m (base-2, scaled), the offset its
+  // exponentials use (0 while the row has no key yet), the accumulators O^T, and this lane's
+  // part of the row sum (fp32, over the lane's keys; the 4 lane groups are added at the end).
+  float m[kPfTiles], m_use[kPfTiles], l[kPfTiles];
   f32x4 acc[kPfTiles][8];
 #pragma unroll
   for (int t = 0; t < kPfTiles; ++t) {
     m[t] = kNegInfP;
+    m_use[t] = 0.f;
     l[t] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -250,55 +254,62 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
         for (int c = 0; c < 4; ++c) sb[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sb[tt]);
       }
     }
-    // online softmax over the step's 32 keys; the scale is folded into exp2's argument. A row
-    // with no key yet (max -inf) uses 0 as its offset: its exponentials and alpha are all 0.
+    // online softmax over the step's 32 keys; the scale is folded into exp2's argument. The
+    // running max moves only when some key exceeds it by more than kPfSlack (log2 units):
+    // exponentials stay below 2^kPfSlack, and on most steps no lane finds such a key, so the
+    // cross-lane max, the new offsets and the rescale are skipped (a wave-uniform branch).
     const int pos = key0 + grp * 4;
     const bool need_mask = key0 + kPfStepKeys - 1 > w_min_limit;
     bf16x8 pf[kPfTiles];
-    float alpha[kPfTiles];
-    bool moved = false;
+    float x[kPfTiles][8];
+    bool over = false;
 #pragma unroll
     for (int tt = 0; tt < kPfTiles; ++tt) {
-      float x[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x[i] = sa[tt][i];
-        x[4 + i] = sb[tt][i];
+        x[tt][i] = sa[tt][i];
+        x[tt][4 + i] = sb[tt][i];
       }
       if (need_mask) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          x[i] = (pos + i <= limit[tt]) ? x[i] : kNegInfP;
-          x[4 + i] = (pos + kPage + i <= limit[tt]) ? x[4 + i] : kNegInfP;
+          x[tt][i] = (pos + i <= limit[tt]) ? x[tt][i] : kNegInfP;
+          x[tt][4 + i] = (pos + kPage + i <= limit[tt]) ? x[tt][4 + i] : kNegInfP;
         }
       }
-      float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-      mx = max_xor32(max_xor16(mx));
-      // the running max moves only when it grows by more than kPfSlack (log2 units): the
-      // exponentials stay below 2^kPfSlack, and the accumulators are rescaled on few steps
-      const float m_cand = mx * p.scale_log2;
-      const float m_new = m_cand > m[tt] + kPfSlack ? m_cand : m[tt];
-      const float m_use = m_new == kNegInfP ? 0.f : m_new;
-      const float a = __builtin_amdgcn_exp2f(m[tt] - m_use);
+      const float lmx = fmaxf(fmaxf(fmaxf(x[tt][0], x[tt][1]), fmaxf(x[tt][2], x[tt][3])),
+                              fmaxf(fmaxf(x[tt][4], x[tt][5]), fmaxf(x[tt][6], x[tt][7])));
+      over |= lmx * p.scale_log2 > m[tt] + kPfSlack;
+    }
+    if (__builtin_amdgcn_ballot_w64(over) != 0) {
+#pragma unroll
+      for (int tt = 0; tt < kPfTiles; ++tt) {
+        float mx = fmaxf(fmaxf(fmaxf(x[tt][0], x[tt][1]), fmaxf(x[tt][2], x[tt][3])),
+                         fmaxf(fmaxf(x[tt][4], x[tt][5]), fmaxf(x[tt][6], x[tt][7])));
+        mx = max_xor32(max_xor16(mx)) * p.scale_log2;
+        const float m_new = mx > m[tt] + kPfSlack ? mx : m[tt];
+        const float mu = m_new == kNegInfP ? 0.f : m_new;
+        // a row with no key before (m = -inf) has zero sums: alpha 0 keeps them zero
+        const float a = __builtin_amdgcn_exp2f(m[tt] - mu);
+        m[tt] = m_new;
+        m_use[tt] = mu;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[tt][j] *= a;
+        l[tt] *= a;
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < kPfTiles; ++tt) {
       float pv[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pv[i] = __builtin_amdgcn_exp2f(fmaf(x[i], p.scale_log2, -m_use));
-      l[tt] = l[tt] * a + (((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7])));
-      m[tt] = m_new;
-      alpha[tt] = a;
-      moved |= a != 1.f;
+      for (int i = 0; i < 8; ++i) pv[i] = __builtin_amdgcn_exp2f(fmaf(x[tt][i], p.scale_log2, -m_use[tt]));
       uint4 w;
       w.x = pack_bf16x2_rne(pv[0], pv[1]);
       w.y = pack_bf16x2_rne(pv[2], pv[3]);
       w.z = pack_bf16x2_rne(pv[4], pv[5]);
       w.w = pack_bf16x2_rne(pv[6], pv[7]);
       pf[tt] = __builtin_bit_cast(bf16x8, w);
-    }
-    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
-#pragma unroll
-      for (int tt = 0; tt < kPfTiles; ++tt)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[tt][j] *= alpha[tt];
+      l[tt] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
     }
     // O^T += V^T . P^T with 16x16x32 MFMAs over the step's 32 keys: lane (r, grp) carries keys
     // 4grp..4grp+3 of both pages, the order P^T's fragment uses; V^T by transpose reads. Keys
