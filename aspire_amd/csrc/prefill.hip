@@ -2,16 +2,19 @@
 //
 // A workgroup of kPfWaves waves takes one query block of one (row, kv head): kPfWaves x 16 x
 // kPfTiles query rows (block_tokens = that / G tokens, G = q heads per kv head), 16 x kPfTiles
-// rows per wave. Every page of the block's keys is read from HBM once per workgroup: two pages
-// at a time (K and V rows of this kv head, 16 KiB) go straight from HBM into one of four LDS
-// stage buffers (buffer_load ... lds, three steps ahead), and each wave runs its tiles over
-// those 32 keys:
+// rows per wave. Default build: 4 waves of two 16-row tiles (128 rows), 168 VGPRs and 48 KiB
+// of LDS, so three workgroups share a CU (three waves per SIMD); each K fragment and each V^T
+// fragment read from LDS feeds both tiles' MFMAs, half the LDS reads per flop of one tile per
+// wave. Every page of the block's keys is read from HBM once per workgroup: two pages at a
+// time (K and V rows of this kv head, 16 KiB) go straight from HBM into one of kPfStages LDS
+// stage buffers (buffer_load ... lds, kPfStages - 1 steps ahead), and each wave runs its tiles
+// over those 32 keys:
 //   * S^T = K . Q^T per page and tile with 4 v_mfma_f32_16x16x32_bf16 (K rows from LDS,
 //     Q fragments in registers); lane (r, grp) holds S^T[key 4grp + i][row r];
 //   * online softmax in fp32 over the 32 keys (exp2 with the scale folded into its argument,
-//     base-2 LSE; row max across the 4 lane groups with permlane swaps), causal masking only
-//     on steps that reach a row's limit; the running max moves only when it grows by more
-//     than kPfSlack, so the accumulators are rescaled on few steps;
+//     base-2 LSE), causal masking only on steps that reach a row's limit; the running max
+//     moves only when some key exceeds it by more than kPfSlack, so on most steps the
+//     cross-lane max and the rescale are skipped;
 //   * O^T += V^T . P^T with 8 v_mfma_f32_16x16x32_bf16 per tile: each lane's 8 keys are
 //     keys 4grp..4grp+3 of both pages (the order S^T left them in), V^T comes from LDS with
 //     transpose reads (ds_read_b64_tr_b16) and is shared by the wave's tiles.
@@ -26,17 +29,17 @@ namespace {
 
 constexpr float kNegInfP = -__builtin_huge_valf();
 #ifndef ASPIRE_PF_WAVES
-#define ASPIRE_PF_WAVES 16
+#define ASPIRE_PF_WAVES 4
 #endif
 #ifndef ASPIRE_PF_TILES
-#define ASPIRE_PF_TILES 1
+#define ASPIRE_PF_TILES 2
 #endif
 #ifndef ASPIRE_PF_RESCALE_SLACK
 #define ASPIRE_PF_RESCALE_SLACK 8
 #endif
 constexpr float kPfSlack = ASPIRE_PF_RESCALE_SLACK;
 #ifndef ASPIRE_PF_STAGES
-#define ASPIRE_PF_STAGES 4
+#define ASPIRE_PF_STAGES 3
 #endif
 constexpr int kPfStages = ASPIRE_PF_STAGES;  // LDS stage buffers (loads run kPfStages - 1 steps ahead)
 static_assert(kPfStages >= 3 && kPfStages <= 8, "3 to 8 stage buffers");
@@ -46,7 +49,7 @@ constexpr int kPfRows = 16 * kPfTiles;      // query rows per wave
 constexpr int kPfBlockRows = kPfWaves * kPfRows;
 constexpr int kPfThreads = 64 * kPfWaves;
 #ifndef ASPIRE_PF_WAVES_PER_EU
-#define ASPIRE_PF_WAVES_PER_EU ((ASPIRE_PF_WAVES + 3) / 4)
+#define ASPIRE_PF_WAVES_PER_EU 3
 #endif
 constexpr int kPfWavesPerEu = ASPIRE_PF_WAVES_PER_EU;  // register budget: waves per SIMD
 constexpr int kPfRowChunks = 16;            // 16-byte chunks per 256-byte key row (one kv head)

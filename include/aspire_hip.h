@@ -462,9 +462,9 @@ typedef struct aspire_prefill_args {
   float sm_scale; int32_t causal;
 } aspire_prefill_args;
 
-/* Tokens per query block for a head configuration: the workgroup's query rows (256 in
- * the default build: 16 waves x 16) / (num_qo_heads / num_kv_heads), or 0 when the GQA
- * group does not divide a wave's query rows (16 in the default build). Host only. */
+/* Tokens per query block for a head configuration: the workgroup's query rows (128 in
+ * the default build: 4 waves x 32) / (num_qo_heads / num_kv_heads), or 0 when the GQA
+ * group does not divide a wave's query rows (32 in the default build). Host only. */
 int aspire_prefill_block_tokens(int32_t num_qo_heads, int32_t num_kv_heads);
 
 int aspire_prefill_run(const aspire_prefill_args* args, void* stream);

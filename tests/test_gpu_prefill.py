@@ -3,6 +3,7 @@
 import pytest
 import torch
 
+from aspire_amd import _lib
 from aspire_amd.attention.holistic_wrapper import build_holistic_dump_jit_args
 from aspire_amd.attention.prefill import BatchPrefillWithPagedKVCacheWrapper
 from aspire_amd.workloads import PAGE, build_step
@@ -46,9 +47,9 @@ def test_dump_refuses_split_rows(gpu):
         w.run(step.q, step.cache, dump, 16, 256)
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (8, 8), (64, 8)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (8, 8), (64, 8), (64, 2)])
 def test_prefill_kernel_head_groups_and_edges(gpu, hq, hkv):
-    """GQA groups 4, 2, 1 and 8 (query blocks of 64, 128, 256 and 32 tokens), rows that end mid-block
+    """GQA groups 4, 2, 1, 8 and 32 (query blocks of 32, 64, 128, 16 and 4 tokens), rows that end mid-block
     and mid-page, a row whose chunk starts at position 0, one with a single new token, and a tail page
     with one valid key; stale slots past each row's length hold NaN keys and +inf values."""
     say("prefill kernel edges", hq, hkv)
@@ -76,7 +77,7 @@ def test_prefill_kernel_head_groups_and_edges(gpu, hq, hkv):
 
 def test_prefill_kernel_separate_kv_tensors_and_gqa16(gpu):
     """K and V in two tensors (the (k_cache, v_cache) form, so the K-to-V distance is an
-    arbitrary allocation offset), and GQA 16 (16-token query blocks)."""
+    arbitrary allocation offset), and GQA 16 (8-token query blocks)."""
     say("prefill kernel separate k/v, GQA 16")
     step = build_step(hq=32, hkv=2, ctx_len=[700, 129, 40], q_len=[300, 129, 7], is_draft=[0] * 3, draft_budget=0,
                       seed=33, device=gpu)
@@ -84,7 +85,7 @@ def test_prefill_kernel_separate_kv_tensors_and_gqa16(gpu):
     v_cache = step.cache[:, 1].contiguous()
     w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD")
     w.plan(step.qo_indptr, step.kv_indptr, step.kv_indices, step.last_page_len, 32, 2, 128, PAGE, causal=True)
-    assert w._pf is not None and w._pf["block_tokens"] * 16 == 256
+    assert w._pf is not None and w._pf["block_tokens"] * 16 == _lib.lib().aspire_prefill_block_tokens(1, 1)
     out, lse = w.run(step.q, (k_cache, v_cache), return_lse=True)
     torch.cuda.synchronize()
     ref_out, ref_lse = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host,
@@ -113,8 +114,8 @@ def test_prefill_kernel_full_chunk_matches_decode_path(gpu, causal):
 
 
 def test_prefill_head_group_outside_the_kernel_takes_the_decode_path(gpu):
-    """GQA 6 (24 query heads over 4 kv heads) does not divide the prefill kernel's 16-row
-    wave tile: plan() routes the rows to the mixed kernel's query tiles, same results."""
+    """GQA 6 (24 query heads over 4 kv heads) does not divide the prefill kernel's 32 query
+    rows per wave: plan() routes the rows to the mixed kernel's query tiles, same results."""
     say("prefill GQA 6")
     step = build_step(hq=24, hkv=4, ctx_len=[500, 90], q_len=[200, 90], is_draft=[0, 0], draft_budget=0, seed=35,
                       device=gpu)
