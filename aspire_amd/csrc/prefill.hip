@@ -60,7 +60,6 @@ constexpr int kPfStepKeys = 2 * kPage;      // keys per step
 
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4p;
 constexpr uint32_t kPfBufferConfig = 0x00020000u;  // gfx9 raw buffer dword 3
-constexpr int kPfOutOfRange = 0x7ffffff0;          // an offset past every descriptor's range
 static_assert(kPfThreads % 64 == 0 && 1024 % kPfThreads == 0, "a step's chunks split evenly over the threads");
 
 // A pointer the whole wave agrees on, kept in scalar registers (buffer descriptors need that).
@@ -93,7 +92,7 @@ struct PrefillParams {
   int64_t o_st, o_sh;
   float* lse;
   int32_t hq, group;
-  float scale_log2;
+  float scale_log2, inv_scale_log2;
   int32_t causal;
 };
 
@@ -110,6 +109,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   uint4* const stages[8] = {stg0, stg1, stg2, stg3, stg4, stg5, stg6, stg7};
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(threadIdx.x >> 6);
+  __builtin_assume(wave >= 0 && wave < kPfWaves);
   const int r = lane & 15, grp = lane >> 4;
   const int G = p.group;
 
@@ -173,11 +173,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   // Per row (lane r of each tile): the running max m (base-2, scaled), the offset its
   // exponentials use (0 while the row has no key yet), the accumulators O^T, and this lane's
   // part of the row sum (fp32, over the lane's keys; the 4 lane groups are added at the end).
-  float m[kPfTiles], m_use[kPfTiles], l[kPfTiles];
+  float m[kPfTiles], m_use[kPfTiles], l[kPfTiles], thr[kPfTiles];
   f32x4 acc[kPfTiles][8];
 #pragma unroll
   for (int t = 0; t < kPfTiles; ++t) {
     m[t] = kNegInfP;
+    thr[t] = kNegInfP;  // (m + kPfSlack) in unscaled score units
     m_use[t] = 0.f;
     l[t] = 0.f;
 #pragma unroll
@@ -190,12 +191,22 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   // kind is uniform across the wave (one scalar buffer descriptor per kind and page) and each
   // lane fetches the global chunk that belongs at its LDS position. K rows are placed with chunk
   // c of row r at c ^ r (conflict-free column reads), V rows at c ^ swz(r) (the transpose reads).
-  // A chunk past vlim (stale slots past kv_len, pages the block does not reach) is requested
-  // with an offset beyond the descriptor's range: the load then writes zeros into LDS.
+  // Rows from vlim on (stale slots past kv_len, pages the block does not reach) lie past their
+  // descriptor's range, which ends after the page's last valid row (row stride >= 256 bytes, so a
+  // 16-byte chunk is wholly inside or wholly outside): such loads write zeros into LDS, and the
+  // waves issue the same instructions on every step.
   const int crow = (wave & 3) * 4 + (lane >> 4), cpos = lane & 15;
-  const int voff_k = crow * int(p.c_st) * 2 + (cpos ^ crow) * 16;
-  const int voff_v = crow * int(p.c_st) * 2 + (cpos ^ pf_swz(crow)) * 16;
-  const int span = wave_uniform(15 * int(p.c_st) * 2 + 256);
+  const int row_bytes = int(p.c_st) * 2;
+  const int voff_k = crow * row_bytes + (cpos ^ crow) * 16;
+  const int voff_v = crow * row_bytes + (cpos ^ pf_swz(crow)) * 16;
+  const char* const head_base = uniform_ptr(reinterpret_cast<const char*>(p.cache + int64_t(g) * p.c_sh));
+  const uint32_t page_bytes = uint32_t(p.c_sp) * 2u;  // below 2^32 (checked on the host)
+  const int64_t kv_bytes = p.c_skv * 2;
+  // byte range of a page whose first key is `first`: its rows below vlim
+  auto page_span = [&](int first) -> int {
+    const int rows_valid = min(max(vlim - first, 0), kPage);
+    return rows_valid > 0 ? (rows_valid - 1) * row_bytes + 256 : 0;
+  };
   typedef const __attribute__((address_space(4))) int32_t* const_ids_t;
   const const_ids_t ids = (const_ids_t)(p.kv_indices + list0);
   auto page_id = [&](int pg) -> int { return ids[min(pg, max(np - 1, 0))]; };
@@ -206,19 +217,18 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   constexpr int kPfWaitN = (kPfStages - 2) * kPer;
   constexpr int kPfWait = (kPfWaitN & 15) | ((kPfWaitN >> 4) << 14) | 0x70;
   auto issue = [&](uint4* buf, int k, int ia, int ib) {
-    const bool edge = k * kPfStepKeys + kPfStepKeys > vlim;
+    const int span_a = page_span(k * kPfStepKeys), span_b = page_span(k * kPfStepKeys + kPage);
+    const char* const page_a = head_base + uint64_t(uint32_t(ia)) * page_bytes;
+    const char* const page_b = head_base + uint64_t(uint32_t(ib)) * page_bytes;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int base = wave * 64 + i * kPfThreads;  // first chunk of this load
       const int kind = base >> 8;
-      const int64_t phys = (kind >> 1) ? ib : ia;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          uniform_ptr(p.cache + phys * p.c_sp + (kind & 1) * p.c_skv + int64_t(g) * p.c_sh), (short)0, span,
-          kPfBufferConfig);
-      int off = (kind & 1) ? voff_v : voff_k;
-      if (edge) off = k * kPfStepKeys + (kind >> 1) * kPage + crow < vlim ? off : kPfOutOfRange;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(buf + base), 16, off,
-                                               0, 0, 0);
+          uniform_ptr(((kind >> 1) ? page_b : page_a) + ((kind & 1) ? kv_bytes : 0)), (short)0,
+          (kind >> 1) ? span_b : span_a, kPfBufferConfig);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(buf + base), 16,
+                                               (kind & 1) ? voff_v : voff_k, 0, 0, 0);
     }
   };
   // LDS release / acquire around the barrier without a memory fence: the fence would also wait
@@ -274,15 +284,16 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
         x[tt][4 + i] = sb[tt][i];
       }
       if (need_mask) {
+        const int d = limit[tt] - pos;  // keys pos + i with i <= d are visible
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          x[tt][i] = (pos + i <= limit[tt]) ? x[tt][i] : kNegInfP;
-          x[tt][4 + i] = (pos + kPage + i <= limit[tt]) ? x[tt][4 + i] : kNegInfP;
+          x[tt][i] = i <= d ? x[tt][i] : kNegInfP;
+          x[tt][4 + i] = kPage + i <= d ? x[tt][4 + i] : kNegInfP;
         }
       }
-      const float lmx = fmaxf(fmaxf(fmaxf(x[tt][0], x[tt][1]), fmaxf(x[tt][2], x[tt][3])),
-                              fmaxf(fmaxf(x[tt][4], x[tt][5]), fmaxf(x[tt][6], x[tt][7])));
-      over |= lmx * p.scale_log2 > m[tt] + kPfSlack;
+      const float lmx = fmaxf(fmaxf(fmaxf(fmaxf(x[tt][0], x[tt][1]), x[tt][2]), fmaxf(fmaxf(x[tt][3], x[tt][4]), x[tt][5])),
+                              fmaxf(x[tt][6], x[tt][7]));
+      over |= lmx > thr[tt];
     }
     if (__builtin_amdgcn_ballot_w64(over) != 0) {
 #pragma unroll
@@ -296,6 +307,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
         const float a = __builtin_amdgcn_exp2f(m[tt] - mu);
         m[tt] = m_new;
         m_use[tt] = mu;
+        thr[tt] = (m_new + kPfSlack) * p.inv_scale_log2;
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[tt][j] *= a;
         l[tt] *= a;
@@ -415,6 +427,9 @@ extern "C" int aspire_prefill_run(const aspire_prefill_args* a, void* stream) {
   ASPIRE_CHECK_ARG(a->num_rows >= 0 && a->total_blocks >= 0, "bad sizes");
   ASPIRE_CHECK_ARG(a->cache_stride_t > 0 && a->cache_stride_t < (int64_t(1) << 26),
                    "cache_stride_t must be positive and below 2^26 elements (a page's rows span 32-bit offsets)");
+  ASPIRE_CHECK_ARG(a->cache_stride_p > 0 && a->cache_stride_p < (int64_t(1) << 31),
+                   "cache_stride_p must be positive and below 2^31 elements");
+  ASPIRE_CHECK_ARG(a->sm_scale > 0.f && a->sm_scale < 1e30f, "sm_scale must be positive and finite");
   if (a->num_rows == 0 || a->total_blocks == 0) return ASPIRE_OK;
   ASPIRE_CHECK_ARG(a->q && a->kv_cache && a->kv_indices && a->kv_indptr && a->kv_last_page_len && a->qo_indptr &&
                        a->block_indptr && a->out,
@@ -448,6 +463,7 @@ extern "C" int aspire_prefill_run(const aspire_prefill_args* a, void* stream) {
   p.hq = a->num_qo_heads;
   p.group = a->num_qo_heads / a->num_kv_heads;
   p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p.inv_scale_log2 = 1.f / p.scale_log2;
   p.causal = a->causal;
   hipLaunchKernelGGL(prefill_kernel, dim3(a->total_blocks * a->num_kv_heads), dim3(kPfThreads), 0,
                      static_cast<hipStream_t>(stream), p);
