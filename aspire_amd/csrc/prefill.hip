@@ -185,51 +185,51 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
     for (int j = 0; j < 8; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Staging. A step's 1024 chunks (16 B) are 4 kinds of 256: page 2s K rows, its V rows, page
-  // 2s + 1 K rows, V rows. They travel from HBM straight into LDS (buffer_load ... lds): wave w's
-  // i-th load writes the stage's chunks w * 64 + i * threads + lane, one contiguous 1 KiB, so a
-  // kind is uniform across the wave (one scalar buffer descriptor per kind and page) and each
-  // lane fetches the global chunk that belongs at its LDS position. K rows are placed with chunk
-  // c of row r at c ^ r (conflict-free column reads), V rows at c ^ swz(r) (the transpose reads).
-  // Rows from vlim on (stale slots past kv_len, pages the block does not reach) lie past their
-  // descriptor's range, which ends after the page's last valid row (row stride >= 256 bytes, so a
-  // 16-byte chunk is wholly inside or wholly outside): such loads write zeros into LDS, and the
-  // waves issue the same instructions on every step.
-  const int crow = (wave & 3) * 4 + (lane >> 4), cpos = lane & 15;
+  // Staging. A step's 16 KiB are 16 slots of 1 KiB (one load of 64 lanes x 16 B each): slot L
+  // holds rows 4 (L & 3) .. 4 (L & 3) + 3 of kind L >> 2 (K rows of page 2s, its V rows, K rows
+  // of page 2s + 1, its V rows) and lands at chunks 64 L .. 64 L + 63 of the stage buffer. They
+  // travel from HBM straight into LDS (buffer_load ... lds). Wave w issues slots w * kPer ..
+  // w * kPer + kPer - 1, all of one kind, so it needs one page id and one scalar buffer
+  // descriptor per step; each lane fetches the global chunk that belongs at its LDS position.
+  // K rows are placed with chunk c of row r at c ^ r (conflict-free column reads), V rows at
+  // c ^ swz(r) (the transpose reads). Rows from vlim on (stale slots past kv_len, pages the
+  // block does not reach) lie past the descriptor's range, which ends after the page's last
+  // valid row (row stride >= 256 bytes, so a 16-byte chunk is wholly inside or wholly outside):
+  // such loads write zeros into LDS, and the waves issue the same instructions on every step.
+  constexpr int kPer = kPfStage / kPfThreads;  // 1 KiB loads per wave and step
+  static_assert(kPer >= 1 && kPer <= 4, "a wave's slots of a step share one kind");
+  const int kind = wave_uniform((wave * kPer) >> 2);
+  const int my_page = kind >> 1;  // 0: page 2s of step s, 1: page 2s + 1
+  const bool is_v = (kind & 1) != 0;
   const int row_bytes = int(p.c_st) * 2;
-  const int voff_k = crow * row_bytes + (cpos ^ crow) * 16;
-  const int voff_v = crow * row_bytes + (cpos ^ pf_swz(crow)) * 16;
-  const char* const head_base = uniform_ptr(reinterpret_cast<const char*>(p.cache + int64_t(g) * p.c_sh));
+  int voff[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int crow = 4 * ((wave * kPer + i) & 3) + (lane >> 4), cpos = lane & 15;
+    voff[i] = crow * row_bytes + (cpos ^ (is_v ? pf_swz(crow) : crow)) * 16;
+  }
+  const char* const kind_base = uniform_ptr(
+      reinterpret_cast<const char*>(p.cache + int64_t(g) * p.c_sh + (is_v ? p.c_skv : int64_t(0))));
   const uint32_t page_bytes = uint32_t(p.c_sp) * 2u;  // below 2^32 (checked on the host)
-  const int64_t kv_bytes = p.c_skv * 2;
-  // byte range of a page whose first key is `first`: its rows below vlim
-  auto page_span = [&](int first) -> int {
-    const int rows_valid = min(max(vlim - first, 0), kPage);
-    return rows_valid > 0 ? (rows_valid - 1) * row_bytes + 256 : 0;
-  };
   typedef const __attribute__((address_space(4))) int32_t* const_ids_t;
   const const_ids_t ids = (const_ids_t)(p.kv_indices + list0);
-  auto page_id = [&](int pg) -> int { return ids[min(pg, max(np - 1, 0))]; };
-  constexpr int kPer = kPfStage / kPfThreads;  // 1 KiB loads per wave and step
+  // this wave's page of step k (clamped to the row's last page; steps past the block load nothing)
+  auto page_id = [&](int k) -> int { return ids[min(2 * k + my_page, max(np - 1, 0))]; };
   // the barrier's wait: this wave's loads of the next step have landed, those of the
   // kPfStages - 2 steps after it may still be in flight (s_waitcnt vmcnt(n) lgkmcnt(0), gfx9
   // encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at 7, lgkmcnt 11:8)
   constexpr int kPfWaitN = (kPfStages - 2) * kPer;
   constexpr int kPfWait = (kPfWaitN & 15) | ((kPfWaitN >> 4) << 14) | 0x70;
-  auto issue = [&](uint4* buf, int k, int ia, int ib) {
-    const int span_a = page_span(k * kPfStepKeys), span_b = page_span(k * kPfStepKeys + kPage);
-    const char* const page_a = head_base + uint64_t(uint32_t(ia)) * page_bytes;
-    const char* const page_b = head_base + uint64_t(uint32_t(ib)) * page_bytes;
+  auto issue = [&](uint4* buf, int k, int id) {
+    // byte range of the page: its rows below vlim
+    const int rows_valid = min(max(vlim - (k * kPfStepKeys + my_page * kPage), 0), kPage);
+    const int span = rows_valid > 0 ? (rows_valid - 1) * row_bytes + 256 : 0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(kind_base + uint64_t(uint32_t(id)) * page_bytes), (short)0, span, kPfBufferConfig);
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int base = wave * 64 + i * kPfThreads;  // first chunk of this load
-      const int kind = base >> 8;
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          uniform_ptr(((kind >> 1) ? page_b : page_a) + ((kind & 1) ? kv_bytes : 0)), (short)0,
-          (kind >> 1) ? span_b : span_a, kPfBufferConfig);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(buf + base), 16,
-                                               (kind & 1) ? voff_v : voff_k, 0, 0, 0);
-    }
+    for (int i = 0; i < kPer; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(buf + (wave * kPer + i) * 64), 16, voff[i], 0, 0, 0);
   };
   // LDS release / acquire around the barrier without a memory fence: the fence would also wait
   // for the step loads in flight (they write LDS). The explicit wait covers this wave's loads of
@@ -353,17 +353,16 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   // on every iteration.
   if (steps > 0) {
 #pragma unroll
-    for (int k = 0; k < kPfStages - 1; ++k) issue(stages[k], k, page_id(2 * k), page_id(2 * k + 1));
-    int na = page_id(2 * (kPfStages - 1)), nb = page_id(2 * (kPfStages - 1) + 1);
+    for (int k = 0; k < kPfStages - 1; ++k) issue(stages[k], k, page_id(k));
+    int next_id = page_id(kPfStages - 1);
     __builtin_amdgcn_s_waitcnt(kPfWait);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     auto body = [&](int s, uint4* cur, uint4* fill) {
-      const int ca = na, cb = nb;
-      na = page_id(2 * (s + kPfStages));
-      nb = page_id(2 * (s + kPfStages) + 1);
-      issue(fill, s + kPfStages - 1, ca, cb);
+      const int id = next_id;
+      next_id = page_id(s + kPfStages);
+      issue(fill, s + kPfStages - 1, id);
       if (s < steps && s * kPfStepKeys <= w_last) compute(cur, s);
       step_barrier();
     };
