@@ -862,36 +862,45 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
   if (p.class_mask & 4) run_class<3>(p, 2, wave, lane, ident, staged, stage_lds);
 }
 
-// Merge of split segments: one wave per (merge item, query row); lane l owns
-// dims 2l, 2l+1 and every lane reads the (wave-uniform) piece LSEs.
+// Merge of split segments. A task is (merge item, 4 query rows): lane l of the wave combines
+// row 4 * t + l / 16 of the item over its pieces, dims 8 (l % 16) .. + 8, so a row's
+// partials are read as 512 contiguous bytes per piece and every row of the launch is served
+// in about one pass of the grid. Tasks past an item's rows end after reading its header.
 constexpr int kMergeRows = 16 * kMaxRowTiles;
+constexpr int kMergeTaskRows = 4;
+constexpr int kMergeTasksPerItem = kMergeRows / kMergeTaskRows;
 
 __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
-  constexpr int kChunk = 16;  // pieces whose loads are issued together
+  constexpr int kChunk = 8;  // pieces whose loads are issued together
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int waves = gridDim.x * 4;
   const int num_merge = wave_uniform(p.plan[3]);
   const MergeItem* items = reinterpret_cast<const MergeItem*>(p.plan + p.merge_off);
-  for (int u = wave; u < num_merge * kMergeRows; u += waves) {
-    const int mi = u / kMergeRows;
-    const int row = u - mi * kMergeRows;
+  const int rsub = lane >> 4, d8 = (lane & 15) * 8;
+  for (int u = wave; u < num_merge * kMergeTasksPerItem; u += waves) {
+    const int mi = u / kMergeTasksPerItem;
+    const int r0 = (u - mi * kMergeTasksPerItem) * kMergeTaskRows;
     const int rows = wave_uniform(items[mi].rows);
-    if (row >= rows) continue;
+    if (r0 >= rows) continue;
+    const int row = min(r0 + rsub, rows - 1);  // lanes past the item's rows repeat its last row
     const int pieces = wave_uniform(items[mi].num_pieces);
     const int64_t first = wave_uniform(items[mi].first_partial_row) + int64_t(row);
     // Running (max, sum, o) over chunks of pieces; within a chunk every LSE and
     // partial load is issued before any is used (one memory round trip).
-    float mx = kNegInf, sum = 0.f, o0 = 0.f, o1 = 0.f;
+    float mx = kNegInf, sum = 0.f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < pieces; k0 += kChunk) {
       const int n = min(kChunk, pieces - k0);
       float lse[kChunk];
-      float2 v[kChunk];
+      float4 va[kChunk], vb[kChunk];
 #pragma unroll
       for (int x = 0; x < kChunk; ++x) {
         const int64_t pr = first + int64_t(k0 + min(x, n - 1)) * rows;
         lse[x] = x < n ? p.part_lse[pr] : kNegInf;
-        v[x] = *reinterpret_cast<const float2*>(p.part_o + pr * kHeadDim + 2 * lane);
+        const float4* src = reinterpret_cast<const float4*>(p.part_o + pr * kHeadDim + d8);
+        va[x] = src[0];
+        vb[x] = src[1];
       }
       float cmx = mx;
 #pragma unroll
@@ -899,26 +908,37 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
       if (cmx == kNegInf) continue;
       const float scale = __builtin_amdgcn_exp2f(mx - cmx);  // 0 when mx = -inf
       sum *= scale;
-      o0 *= scale;
-      o1 *= scale;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] *= scale;
 #pragma unroll
       for (int x = 0; x < kChunk; ++x) {
         const float w = __builtin_amdgcn_exp2f(lse[x] - cmx);  // 0 for padding / empty pieces
         sum += w;
-        o0 += w * v[x].x;
-        o1 += w * v[x].y;
+        o[0] += w * va[x].x;
+        o[1] += w * va[x].y;
+        o[2] += w * va[x].z;
+        o[3] += w * va[x].w;
+        o[4] += w * vb[x].x;
+        o[5] += w * vb[x].y;
+        o[6] += w * vb[x].z;
+        o[7] += w * vb[x].w;
       }
       mx = cmx;
     }
+    if (r0 + rsub >= rows) continue;
     const float inv = sum > 0.f ? 1.f / sum : 0.f;
     const int G = p.group;
     const int qi = row / G;
     const int g = wave_uniform(items[mi].bg) & 255;
     const int head = g * G + (row - qi * G);
     const int token = wave_uniform(items[mi].q_start) + qi;
-    uint16_t* dst = p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + 2 * lane;
-    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2_rne(o0 * inv, o1 * inv);
-    if (lane == 0 && p.lse != nullptr)
+    uint4 w;
+    w.x = pack_bf16x2_rne(o[0] * inv, o[1] * inv);
+    w.y = pack_bf16x2_rne(o[2] * inv, o[3] * inv);
+    w.z = pack_bf16x2_rne(o[4] * inv, o[5] * inv);
+    w.w = pack_bf16x2_rne(o[6] * inv, o[7] * inv);
+    *reinterpret_cast<uint4*>(p.out + int64_t(token) * p.o_st + int64_t(head) * p.o_sh + d8) = w;
+    if ((lane & 15) == 0 && p.lse != nullptr)
       p.lse[int64_t(token) * p.hq + head] = sum > 0.f ? mx + __builtin_log2f(sum) : kNegInf;
   }
 }
