@@ -117,7 +117,10 @@ static_assert(kAttnWavesPerBlock == 4, "staged K/V assumes 4-wave workgroups (4 
 #ifndef ASPIRE_DIRECT_VT_MIN_NT
 #define ASPIRE_DIRECT_VT_MIN_NT 4
 #endif
-constexpr int kLdsChunks = kStageChunks + (ASPIRE_DIRECT_VT_MIN_NT <= kMaxRowTiles ? kAttnWavesPerBlock * kVtChunks : 0);
+constexpr int kVtScratchChunks = ASPIRE_DIRECT_VT_MIN_NT <= kMaxRowTiles ? kAttnWavesPerBlock * kVtChunks : 0;
+// Per-wave page scores of the key-mean epilogue (64 pages, fp32), after the other areas.
+constexpr int kScoreChunks = kAttnWavesPerBlock * 64 / 4;
+constexpr int kLdsChunks = kStageChunks + kVtScratchChunks + kScoreChunks;
 // Issue the next page's V load right after QK^T (with K's) rather than after P.V.
 #ifndef ASPIRE_DIRECT_VT_EARLY_V
 #define ASPIRE_DIRECT_VT_EARLY_V 0
@@ -296,8 +299,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   // smallest causal limit of the item's rows (its first query token)
   const int min_limit = p.causal ? min(kv_len - it.q_len, kv_len - 1) : kv_len - 1;
   const bool do_dump = p.dump_kind != 0 && (p.dump_flags == nullptr || p.dump_flags[b] != 0);
-  const bool do_score = p.page_scores != nullptr && it.q_len == 1;
-  float score_buf = 0.f;
+  // (q_len 1 rows have at most 16 query rows: one tile)
+  const bool do_score = NT == 1 && p.page_scores != nullptr && it.q_len == 1;
+  // key-mean epilogue: this lane's 4-key partial sums of the last 4 pages (sc0 newest) and
+  // the wave's 64-page score block in LDS
+  float sc0 = 0.f, sc1 = 0.f, sc2 = 0.f, sc3 = 0.f;
+  float score_buf = 0.f;  // the VALU draft path's 64-page block (lane = page slot)
+  float* const score_lds = reinterpret_cast<float*>(stage_lds + kStageChunks + kVtScratchChunks) +
+                           ((threadIdx.x >> 6) & (kAttnWavesPerBlock - 1)) * 64;
   const int dump_slots = p.dump_kind == 2 ? 2 : 1;
 
   // Page ids are read with scalar loads (constant address space): they are
@@ -450,27 +459,46 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
               if (base_pos + i < kv_len) store_dump(p, base + base_pos + i, s[t][i]);
           }
         }
-        if (do_score && t == 0) {
-          float rs = 0.f;
+        if (NT == 1 && do_score && t == 0) {
+          // Key-mean score of a page: max over the group's heads of sum_{valid keys} q.k / count.
+          // Each lane adds its 4 keys; the cross-lane sums run once per 4 pages: two
+          // half-wave and one 16-lane exchange turn the 4 pages' partials into page
+          // pg - 3 + grp's totals in lane group grp, then the heads' max (lanes r < G) and
+          // one LDS write per group. A partial batch at the piece's end rewrites the slots of
+          // pages already written (same values) or slots no store reads.
+          float rs = (s[t][0] + s[t][1]) + (s[t][2] + s[t][3]);
+          if (pg * 16 + 16 > kv_len) {
+            rs = 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) rs += (base_pos + i < kv_len) ? s[t][i] : 0.f;
-          rs = add_xor32(add_xor16(rs));
-          const int cnt = min(16, kv_len - pg * 16);
-          float val = (r < G) ? (cnt == 16 ? rs * 0.0625f : rs / float(cnt)) : kNegInf;
-          // max over the group's heads (lanes r < G of each row)
-          if (G > 1) val = fmaxf(val, dpp_xor1(val));
-          if (G > 2) val = fmaxf(val, dpp_xor2(val));
-          if (G > 4) val = fmaxf(val, shfl_xor_f(val, 4));
-          if (G > 8) val = fmaxf(val, shfl_xor_f(val, 8));
-          // Lane 0 holds the page's score. Lane (pg - pb) % 64 keeps it; the
-          // wave writes 64 pages at once (one coalesced store instead of a
-          // single-lane store per page, which would share vmcnt with the K/V
-          // loads in flight).
+            for (int i = 0; i < 4; ++i) rs += (base_pos + i < kv_len) ? s[t][i] : 0.f;
+          }
+          sc3 = sc2;
+          sc2 = sc1;
+          sc1 = sc0;
+          sc0 = rs;
           const int slot = (pg - pb) & 63;
-          const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val), 0));
-          score_buf = lane == slot ? v0 : score_buf;
-          if (slot == 63 || pg == pe - 1) {
-            if (lane <= slot) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + (pg - slot) + lane] = score_buf;
+          if ((slot & 3) == 3 || pg == pe - 1) {
+            const auto h0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(sc3), __float_as_uint(sc1), false, false);
+            const auto h1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(sc2), __float_as_uint(sc0), false, false);
+            const float a0 = __uint_as_float(h0[0]) + __uint_as_float(h0[1]);  // pages pg-3 (low half), pg-1 (high)
+            const float a1 = __uint_as_float(h1[0]) + __uint_as_float(h1[1]);  // pages pg-2 (low half), pg (high)
+            const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(a0), __float_as_uint(a1), false, false);
+            const float tot = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // page pg - 3 + grp
+            const int page = pg - 3 + grp;
+            const int cnt = min(16, kv_len - page * 16);
+            float val = (r < G) ? (cnt >= 16 ? tot * 0.0625f : tot / float(max(cnt, 1))) : kNegInf;
+            // max over the group's heads (lanes r < G of each 16-lane group)
+            if (G > 1) val = fmaxf(val, dpp_xor1(val));
+            if (G > 2) val = fmaxf(val, dpp_xor2(val));
+            if (G > 4) val = fmaxf(val, shfl_xor_f(val, 4));
+            if (G > 8) val = fmaxf(val, shfl_xor_f(val, 8));
+            if (r == 0) score_lds[(page - pb) & 63] = val;
+            // One coalesced store per 64 pages (a store per page would share vmcnt
+            // with the K/V loads in flight).
+            if (slot == 63 || pg == pe - 1) {
+              const float v = score_lds[lane];  // a wave's LDS accesses complete in order
+              if (lane <= slot) p.page_scores[int64_t(b * p.hkv + g) * p.ps_stride + (pg - slot) + lane] = v;
+            }
           }
         }
 
