@@ -48,7 +48,7 @@ struct AttnParams {
   float scale_log2;
   int32_t causal;
   void* dump;
-  int32_t dump_kind, dump_f32;
+  int32_t dump_kind, dump_f32, dump_vec;
   int64_t dump_stride;
   int32_t dump_heads;
   const int32_t* dump_flags;
@@ -308,6 +308,21 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   float* const score_lds = reinterpret_cast<float*>(stage_lds + kStageChunks + kVtScratchChunks) +
                            ((threadIdx.x >> 6) & (kAttnWavesPerBlock - 1)) * 64;
   const int dump_slots = p.dump_kind == 2 ? 2 : 1;
+  // Dump entry of each tile's row: the lane's element offset of key 0, or -1 for rows that
+  // write nothing (kind 1: a row's last query; kind 2: its first and last).
+  int64_t dump_at[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    dump_at[t] = -1;
+    const int qi = row_qi[t];
+    if (do_dump && qi >= 0) {
+      const int slot = p.dump_kind == 2 ? (qi == 0 ? 0 : (qi == it.q_len - 1 ? 1 : -1)) : (qi == it.q_len - 1 ? 0 : -1);
+      if (slot >= 0) {
+        const int head = g * G + (t * 16 + r - qi * G);
+        dump_at[t] = (int64_t(b * p.dump_heads + head) * dump_slots + slot) * p.dump_stride;
+      }
+    }
+  }
 
   // Page ids are read with scalar loads (constant address space): they are
   // wave-uniform, and scalar loads are tracked by lgkmcnt, so waiting for an id
@@ -443,20 +458,24 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       float alpha[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        if (do_dump && row_qi[t] >= 0) {
-          const int qi = row_qi[t];
-          int slot = -1;
-          if (p.dump_kind == 2)
-            slot = qi == 0 ? 0 : (qi == it.q_len - 1 ? 1 : -1);
-          else if (qi == it.q_len - 1)
-            slot = 0;
-          if (slot >= 0) {
-            const int head = g * G + (t * 16 + r - qi * G);
-            const int64_t base =
-                (int64_t(b * p.dump_heads + head) * dump_slots + slot) * p.dump_stride;
+        if (do_dump && dump_at[t] >= 0) {
+          // the lane's 4 consecutive keys of its row: one 8-byte (fp16) or 16-byte (fp32)
+          // store when all 4 are valid and the entry is aligned, else one store per key
+          const int64_t at = dump_at[t] + base_pos;
+          if (p.dump_vec && base_pos + 4 <= kv_len) {
+            if (p.dump_f32) {
+              *reinterpret_cast<float4*>(static_cast<float*>(p.dump) + at) = make_float4(s[t][0], s[t][1], s[t][2], s[t][3]);
+            } else {
+              typedef __attribute__((ext_vector_type(4))) _Float16 half4;
+              half4 h;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) h[i] = static_cast<_Float16>(s[t][i]);
+              *reinterpret_cast<half4*>(static_cast<_Float16*>(p.dump) + at) = h;
+            }
+          } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if (base_pos + i < kv_len) store_dump(p, base + base_pos + i, s[t][i]);
+              if (base_pos + i < kv_len) store_dump(p, at + i, s[t][i]);
           }
         }
         if (NT == 1 && do_score && t == 0) {
@@ -1092,6 +1111,9 @@ int attention_run_impl(const aspire_plan_layout* layout, const aspire_attention_
   p.dump_kind = a->dump_kind;
   p.dump_f32 = a->dump_dtype == 1;
   p.dump_stride = a->dump_kv_stride;
+  // 4 consecutive keys of a row form one aligned vector (8 or 16 bytes) when the row stride
+  // is a multiple of 4 entries and the buffer is 16-byte aligned
+  p.dump_vec = a->dump_kind != 0 && a->dump_kv_stride % 4 == 0 && al16(a->dump);
   p.dump_heads = a->dump_num_heads;
   p.dump_flags = a->dump_mode_flags;
   p.page_scores = a->page_scores;
