@@ -34,6 +34,18 @@ __device__ __forceinline__ uint32_t bf16_key(uint16_t b) {
   return (b & 0x8000u) ? (~uint32_t(b) & 0xffffu) : (uint32_t(b) | 0x8000u);
 }
 
+// The keys of two packed bf16 values at once (16-bit packed integer operations): negative
+// values flip every bit, others set the sign bit, and -0 (whose flipped bits give 0x7fff, a key
+// no other value has) moves up to +0's key 0x8000.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_keys(uint32_t w) {
+  const u16x2 b = __builtin_bit_cast(u16x2, w);
+  const u16x2 sgn = __builtin_bit_cast(u16x2, __builtin_bit_cast(i16x2, b) >> 15);
+  const u16x2 k = b ^ (sgn | (u16x2){0x8000, 0x8000});
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(k, (k + (u16x2){1, 1}) & (u16x2){0x8000, 0x8000}));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
@@ -186,11 +198,11 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
       const uint4* rv = reinterpret_cast<const uint4*>(row);
       for (int v = t; v < nv; v += kTkThreads) {
         const uint4 w = rv[v];
-        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+        const uint32_t u[4] = {bf16x2_keys(w.x), bf16x2_keys(w.y), bf16x2_keys(w.z), bf16x2_keys(w.w)};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          f(8 * v + 2 * e, bf16_key(uint16_t(u[e] & 0xffffu)));
-          f(8 * v + 2 * e + 1, bf16_key(uint16_t(u[e] >> 16)));
+          f(8 * v + 2 * e, u[e] & 0xffffu);
+          f(8 * v + 2 * e + 1, u[e] >> 16);
         }
       }
       for (int i = (nv << 3) + t; i < V; i += kTkThreads) f(i, bf16_key(row[i]));
@@ -317,8 +329,8 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
   uint16_t* vout = p.values + int64_t(blockIdx.x) * p.k;
   int64_t* iout = p.ids + int64_t(blockIdx.x) * p.k;
   for (int j = t; j < p.k; j += kTkThreads) {
-    if (j < kk) {
-      const uint32_t id = 0xffffffffu - uint32_t(cand[j] & 0xffffffffu);
+    const uint32_t id = 0xffffffffu - uint32_t(cand[j] & 0xffffffffu);
+    if (j < kk && id < uint32_t(V)) {  // (ids come from the row: the bound is a guard)
       vout[j] = row[id];  // the logit's own bits (a -0 stays -0)
       iout[j] = int64_t(id) + p.vocab_start;
     } else {

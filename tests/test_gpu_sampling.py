@@ -33,12 +33,14 @@ def test_topk_candidates_exact(gpu, rows, vocab, k, start):
     assert torch.equal(vals.cpu().view(torch.int16), ref_v.view(torch.int16))
 
 
-@pytest.mark.parametrize("case", ["continuous", "all_equal", "misaligned", "equal_blocks"])
+@pytest.mark.parametrize("case", ["continuous", "all_equal", "misaligned", "equal_blocks", "outliers"])
 def test_topk_candidates_paths(gpu, case):
     """Both collection paths and both load widths: continuous logits (few ties: one pass over every
     key >= the k-th), rows of one repeated value and rows where the boundary value repeats
     thousands of times (ties overflow the candidate buffer: the id-ordered tie ranking), and a
-    view whose rows start 2 bytes past a 16-byte boundary (2-byte loads)."""
+    view whose rows start 2 bytes past a 16-byte boundary (2-byte loads); and rows whose largest
+    keys are a few outliers, so the histogram from one bin below the maximum's bin holds fewer
+    than k keys and is redone over every bin."""
     say("topk candidates path", case)
     g = torch.Generator().manual_seed(11)
     rows, vocab, k = 6, 20016, 100
@@ -49,6 +51,11 @@ def test_topk_candidates_paths(gpu, case):
         logits[1] = -3.0
     elif case == "misaligned":
         logits = (torch.randn(rows, vocab, generator=g) * 3).round().to(torch.bfloat16)
+    elif case == "outliers":
+        logits = torch.randn(rows, vocab, generator=g)
+        logits[:, 100:110] = 1000.0                # 10 keys far above the rest, k = 100
+        logits[2, 7] = -1000.0
+        logits = logits.to(torch.bfloat16)
     else:
         logits = torch.zeros(rows, vocab).to(torch.bfloat16)
         logits[:, ::7] = 1.0                       # ~2,860 keys tie at the boundary value
