@@ -71,6 +71,9 @@ def parse():
                          "step); 2: refresh layer; 3: the full 36-layer decode step alone; 4: the long-context "
                          "layer at --draft-frac")
     ap.add_argument("--draft-frac", type=float, default=0.5, help="config 4: fraction of drafting rows")
+    ap.add_argument("--class-mask", type=int, default=0,
+                    help="config 4: time only the attention launch of these row-tile classes (bit c-1 for class c: "
+                         "<=16, <=32, <=48 query rows), no merge; value counts their KV bytes (for per-class counters)")
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed CPU-baseline runs per config (after 2 warm-ups)")
@@ -253,6 +256,14 @@ def main():
         def run_step():
             w.run(step.q, cache, out=out, page_scores=selector.page_scores)
             selector.select(npg, step.block_table)
+    elif args.config == 4 and args.class_mask:
+        run_step = attention_only(w, step.q, cache, out, class_mask=args.class_mask)
+        rows = step.q_len * (step.hq // step.hkv)
+        cls = np.where(rows <= 16, 0, np.where(rows <= 32, 1, 2))
+        keep = np.array([(args.class_mask >> c) & 1 for c in range(3)], dtype=bool)[cls]
+        kvl = step.kv_len_host.numpy()[: step.batch].astype(np.int64)
+        nbytes = {"kv": int(kvl[keep].sum()) * step.hkv * 128 * 4, "qo": 0, "indices": 0}
+        nbytes["total"] = nbytes["kv"]
     elif args.config == 4:
         def run_step():
             w.run(step.q, cache, out=out)
@@ -271,7 +282,7 @@ def main():
     value = nbytes["total"] / (ms * 1e-3) / 1e9
 
     # dominant kernel alone: mixed attention (no merge), same plan, same stream
-    attn = attention_only(w, step.q, cache, out)
+    attn = attention_only(w, step.q, cache, out, class_mask=(args.class_mask or None) if args.config == 4 else None)
     for _ in range(3):
         attn()
     attn_ms, attn_per = timed_steps(attn, args.steps, stream)
@@ -317,6 +328,9 @@ def main():
                     f"U[65536, 131072], draft fraction {args.draft_frac} (256-page drafts, verify q_len U{{2..9}}); "
                     "attention + split-KV merge")
         metric = f"long-context layer HBM GB/s (DS-Llama-8B shape, B=16, ctx U[64k,128k], f={args.draft_frac})"
+        if args.class_mask:
+            workload += f"; attention launch of row-tile class mask {args.class_mask} only (KV bytes of those rows)"
+            metric += f", class mask {args.class_mask}"
     line = {
         "metric": metric,
         "value": round(value, 1),
