@@ -909,41 +909,51 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
   if (p.class_mask & 4) run_class<3>(p, 2, wave, lane, ident, staged, stage_lds);
 }
 
-// Merge of split segments. A task is (merge item, 4 query rows): lane l of the wave combines
-// row 4 * t + l / 16 of the item over its pieces, dims 8 (l % 16) .. + 8, so a row's
-// partials are read as 512 contiguous bytes per piece and every row of the launch is served
-// in about one pass of the grid. Tasks past an item's rows end after reading its header.
-constexpr int kMergeRows = 16 * kMaxRowTiles;
-constexpr int kMergeTaskRows = 4;
-constexpr int kMergeTasksPerItem = kMergeRows / kMergeTaskRows;
+// Merge of split segments. A task is (merge item, 4 units), one unit per 16-lane group: a
+// unit is (row, piece group) of the item's row range, and lane l of a group combines dims
+// 8 (l % 16) .. + 8 of its row over the pieces of its piece group, so a row's partials are
+// read as 512 contiguous bytes per piece. Items with more pieces than one round of loads
+// covers (kMergeChunk) come as row ranges of at most 24 or 12 rows whose rows split their
+// pieces over s = 2 or 4 adjacent groups (pieces g, g + s, ...); the groups of a row then
+// combine their (max, sum, o) states by cross-lane exchanges. A 36-row item of 69 pieces
+// thus takes 36 waves with three rounds of loads each instead of 9 waves with nine. Tasks
+// past an item's units end after reading its header.
+constexpr int kMergeTaskUnits = 4;
+constexpr int kMergeTasksPerItem = kMergeRows / kMergeTaskUnits;
 
 __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
-  constexpr int kChunk = 8;  // pieces whose loads are issued together
+  constexpr int kChunk = kMergeChunk;  // pieces whose loads are issued together
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int waves = gridDim.x * 4;
   const int num_merge = wave_uniform(p.plan[3]);
   const MergeItem* items = reinterpret_cast<const MergeItem*>(p.plan + p.merge_off);
-  const int rsub = lane >> 4, d8 = (lane & 15) * 8;
+  const int gsub = lane >> 4, d8 = (lane & 15) * 8;
   for (int u = wave; u < num_merge * kMergeTasksPerItem; u += waves) {
     const int mi = u / kMergeTasksPerItem;
-    const int r0 = (u - mi * kMergeTasksPerItem) * kMergeTaskRows;
+    const int v0 = (u - mi * kMergeTasksPerItem) * kMergeTaskUnits;
     const int rows = wave_uniform(items[mi].rows);
-    if (r0 >= rows) continue;
-    const int row = min(r0 + rsub, rows - 1);  // lanes past the item's rows repeat its last row
+    const int row_count = wave_uniform(items[mi].row_count);
     const int pieces = wave_uniform(items[mi].num_pieces);
+    const int s = merge_piece_groups(pieces, row_count);  // piece groups per row
+    if (v0 >= row_count * s) continue;
+    const int v = v0 + gsub;
+    // units past the item's rows repeat its last row
+    const int row = wave_uniform(items[mi].row_begin) + min(v / s, row_count - 1);
+    const int pg = v & (s - 1);
+    const int my_pieces = (pieces - pg + s - 1) / s;
     const int64_t first = wave_uniform(items[mi].first_partial_row) + int64_t(row);
-    // Running (max, sum, o) over chunks of pieces; within a chunk every LSE and
+    // Running (max, sum, o) over chunks of the group's pieces; within a chunk every LSE and
     // partial load is issued before any is used (one memory round trip).
     float mx = kNegInf, sum = 0.f;
     float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < pieces; k0 += kChunk) {
-      const int n = min(kChunk, pieces - k0);
+    for (int k0 = 0; k0 < my_pieces; k0 += kChunk) {
+      const int n = min(kChunk, my_pieces - k0);
       float lse[kChunk];
       float4 va[kChunk], vb[kChunk];
 #pragma unroll
       for (int x = 0; x < kChunk; ++x) {
-        const int64_t pr = first + int64_t(k0 + min(x, n - 1)) * rows;
+        const int64_t pr = first + int64_t(pg + (k0 + min(x, n - 1)) * s) * rows;
         lse[x] = x < n ? p.part_lse[pr] : kNegInf;
         const float4* src = reinterpret_cast<const float4*>(p.part_o + pr * kHeadDim + d8);
         va[x] = src[0];
@@ -972,7 +982,23 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
       }
       mx = cmx;
     }
-    if (r0 + rsub >= rows) continue;
+    // Piece groups of a row sit in adjacent 16-lane groups: fold them pairwise.
+    for (int mask = 16; mask < 16 * s; mask <<= 1) {
+      const float mo = __shfl_xor(mx, mask);
+      const float so = __shfl_xor(sum, mask);
+      float oo[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) oo[i] = __shfl_xor(o[i], mask);
+      const float mn = fmaxf(mx, mo);
+      if (mn != kNegInf) {
+        const float a = __builtin_amdgcn_exp2f(mx - mn), b = __builtin_amdgcn_exp2f(mo - mn);
+        sum = sum * a + so * b;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = o[i] * a + oo[i] * b;
+        mx = mn;
+      }
+    }
+    if (pg != 0 || v / s >= row_count) continue;
     const float inv = sum > 0.f ? 1.f / sum : 0.f;
     const int G = p.group;
     const int qi = row / G;

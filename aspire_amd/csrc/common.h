@@ -77,7 +77,10 @@ struct WorkItem {
 // head's rows instead of staging shared pages through LDS.
 constexpr int32_t kItemDirect = 1 << 16;
 
-// A split (row, kv head) segment whose pieces are merged (8 x int32).
+// Rows [row_begin, row_begin + row_count) of a split (row, kv head) segment whose pieces
+// are merged (8 x int32). A segment with more pieces than one round of the merge kernel's
+// loads (kMergeChunk) is cut into row ranges of at most kMergeRows / s rows, s = 2 or 4, so
+// that s lane groups can share each row's pieces within the kernel's task budget.
 struct MergeItem {
   int32_t q_start;
   int32_t q_len;
@@ -85,9 +88,19 @@ struct MergeItem {
   int32_t first_partial_row;
   int32_t num_pieces;
   int32_t rows;         // q_len * group; partials of piece i start at first + i*rows
-  int32_t pad0;
-  int32_t pad1;
+  int32_t row_begin;
+  int32_t row_count;
 };
+constexpr int kMergeRows = 16 * kMaxRowTiles;  // rows of one merge item at most
+constexpr int kMergeChunk = 8;                 // pieces per round of a lane's merge loads
+
+// Piece groups per row for a merge item of `pieces` pieces and `row_count` rows (1, 2 or 4).
+__host__ __device__ inline int merge_piece_groups(int pieces, int row_count) {
+  int s = 1;
+  if (pieces > kMergeChunk && 2 * row_count <= kMergeRows) s = 2;
+  if (pieces > 2 * kMergeChunk && 4 * row_count <= kMergeRows) s = 4;
+  return s;
+}
 
 // Fixed offsets (int32 units) of the plan in the int workspace.
 struct PlanOffsets {

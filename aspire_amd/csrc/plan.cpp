@@ -78,7 +78,7 @@ extern "C" int aspire_plan_layout_init(int32_t num_cus, int32_t waves_per_cu, in
   aspire_plan_layout L;
   L.num_waves = waves;
   L.max_items = 4 * waves + 8192;
-  L.max_merge = 2 * waves + 8192;
+  L.max_merge = 8 * waves + 16384;  // a split segment may be cut into up to 4 row ranges
   L.head_dim = head_dim;
   PlanOffsets o = plan_offsets(L);
   while (o.total * 4 > int_ws_bytes && L.max_items > waves + 64) {
@@ -244,11 +244,17 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
             sc.items.emplace_back(static_cast<int32_t>(((j + rot) % slots) * hpu + gg), it);
           }
         }
-        if (pieces > 1)
+        if (pieces > 1) {
+          // row ranges small enough for the merge kernel's piece groups
+          const int span = pieces > 2 * kMergeChunk ? kMergeRows / 4
+                           : pieces > kMergeChunk   ? kMergeRows / 2
+                                                    : kMergeRows;
           for (int gg = 0; gg < hpu; ++gg)
-            sc.merges.push_back(MergeItem{s.q_start, s.q_len, s.bg + gg,
-                                          static_cast<int32_t>(first + int64_t(gg) * pieces * s.rows),
-                                          pieces, s.rows, 0, 0});
+            for (int r0 = 0; r0 < s.rows; r0 += span)
+              sc.merges.push_back(MergeItem{s.q_start, s.q_len, s.bg + gg,
+                                            static_cast<int32_t>(first + int64_t(gg) * pieces * s.rows),
+                                            pieces, s.rows, r0, std::min(span, s.rows - r0)});
+        }
         seg_off = e;
       }
       if (pr <= L.partial_rows_cap || s_eff == 1) {

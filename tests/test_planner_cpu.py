@@ -118,12 +118,23 @@ def check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv, per_head=False, causal=Tr
             for t0, tq, keys in expected_tiles(qo[b + 1] - qo[b], kvl[seg], group, causal):
                 for p in range((keys + 15) // 16):
                     assert (b, g, t0, p) in seen
-    # merge items reference the split pieces
+    # merge items reference the split pieces; their row ranges cover each split segment's rows
+    # once, in ranges the merge kernel's piece groups fit (48 rows, or 24 / 12 rows for items of
+    # more than 8 / 16 pieces)
+    covered = {}
     for m in merges:
-        q_start, q_len, bg, first, pieces, rows = m[:6].tolist()
+        q_start, q_len, bg, first, pieces, rows, row_begin, row_count = m.tolist()
         assert pieces >= 2 and rows == q_len * group
+        assert 0 <= row_begin and 0 < row_count and row_begin + row_count <= rows
+        assert row_count <= (12 if pieces > 16 else 24 if pieces > 8 else 48)
         for k in range(pieces):
             assert first + k * rows in partial_rows
+        got = covered.setdefault((q_start, bg, first), set())
+        assert got.isdisjoint(range(row_begin, row_begin + row_count))
+        got.update(range(row_begin, row_begin + row_count))
+    for (q_start, bg, first), got in covered.items():
+        q_len = next(int(m[1]) for m in merges if (m[0], m[2], m[3]) == (q_start, bg, first))
+        assert got == set(range(q_len * group))
     return seen
 
 
@@ -287,3 +298,32 @@ def test_rejects_gqa_group_wider_than_three_tiles():
     assert "at most 48" in _lib.lib().aspire_last_error().decode()
     # the widest accepted group (48 q heads per kv head) still plans
     plan(lay, qo, kvp, kvl, 48, 1)
+
+
+def test_merge_row_ranges_config3_layer():
+    """A config-3 mixed layer (64 rows, contexts U[8k, 32k], per-head top-128 draft lists, verify
+    q_len U{2..9}) on 256 CUs: the two long q_len-9 rows of the 3-tile class are split into
+    60-69 pieces, and their 36-row merges come as row ranges of 12 rows, so that four lane groups
+    share each row's pieces; items of at most 8 pieces stay whole."""
+    from aspire_amd.workloads import PAGE, config3_rows
+
+    ctx, ql, dr = config3_rows(seed=0)
+    hq, hkv = 32, 8
+    starts, pages, kvl = [], [], []
+    pos = 0
+    for b in range(len(ctx)):
+        n = (int(ctx[b]) + PAGE - 1) // PAGE
+        for g in range(hkv):
+            starts.append(pos + g * 128 if dr[b] else pos)
+            pages.append(128 if dr[b] else n)
+            kvl.append(127 * PAGE + int(ctx[b]) - (n - 1) * PAGE if dr[b] else int(ctx[b]))
+        pos += 128 * hkv if dr[b] else n
+    qo = np.concatenate([[0], np.cumsum(ql)])
+    lay = layout(num_cus=256, waves_per_cu=4)
+    buf, info = plan_segments(lay, qo, starts, pages, kvl, hq, hkv)
+    check_cover(lay, buf, info, qo, None, np.array(kvl), hq, hkv, per_head=True, seg_start=np.array(starts))
+    _, merges = decode(lay, buf, info)
+    long = merges[merges[:, 4] > 16]
+    assert len(long) and (long[:, 7] <= 12).all() and (long[:, 5] == 36).any()
+    short = merges[merges[:, 4] <= 8]
+    assert (short[:, 6] == 0).all() and (short[:, 7] == short[:, 5]).all()
