@@ -1,13 +1,15 @@
 // (f4) Token sampling and speculative verification for gfx950.
 //
 // * topk_candidates_kernel: the top_k logits of a row and their ids, descending, ties to the
-//   lower id. One 1024-thread workgroup per row, 16-byte loads. Radix select on 16-bit
-//   order-preserving keys of the bf16 logits: a histogram of the high byte, then of the low
-//   byte among the boundary bin, gives the k-th key exactly; one pass collects every key at or
-//   above it and a bitonic sort in LDS orders them (ties by id), so the first top_k are the
-//   answer. When the boundary key repeats so often that the candidates overflow LDS, an
-//   ordered pass ranks its ties by id instead. Histograms use 64 LDS sub-histograms
-//   (wave, lane % 4) so lanes with equal keys rarely serialise on one counter.
+//   lower id. One 1024-thread workgroup per row, 16-byte loads; rows of up to 155,648 logits
+//   are read once and kept in registers as keys. Radix select on 16-bit order-preserving keys
+//   of the bf16 logits: a histogram of the high byte, then of the low byte among the boundary
+//   bin, gives the k-th key exactly (each boundary from suffix sums in one wave); one pass
+//   collects every key at or above it and a bitonic sort (in one wave's registers up to 64
+//   candidates, else in LDS) orders them (ties by id), so the first top_k are the answer.
+//   When the boundary key repeats so often that the candidates overflow LDS, an ordered pass
+//   ranks its ties by id instead. Histograms use 256 LDS sub-histograms (wave, lane % 16) of
+//   16-bit counters, so lanes with equal keys rarely serialise on one counter.
 // * logits_pipe_kernel: temperature, softmax and top-p renormalisation of one row in LDS.
 // * sample_kernel / chain_kernel / verify_kernel: inverse-CDF draws with the uniforms given
 //   (a contiguous chunk per thread, chunk sums scanned in thread order, so the prefix sums
@@ -173,94 +175,160 @@ struct TopKParams {
   int64_t* ids;      // [rows, k]
 };
 
-constexpr int kTkThreads = 1024;                 // one workgroup of 16 waves per row
-constexpr int kTkSubHists = (kTkThreads / 64) * 4;  // sub-histograms: (wave, lane % 4)
-constexpr int kTkCandCap = 2048;                  // candidates sorted in LDS
+constexpr int kTkThreads = 1024;                     // one workgroup of 16 waves per row
+constexpr int kTkSubHists = (kTkThreads / 64) * 16;   // sub-histograms: (wave, lane % 16)
+constexpr int kTkHistStride = 129;  // 128 dwords of two 16-bit counters, +1 so sub-histograms start on other banks
+constexpr int kTkCandCap = 2048;    // candidates sorted in LDS
+constexpr int kTkResident = 19;     // 16-byte vectors per thread held in registers (rows up to 155,648 logits)
+constexpr int kTkMaxVocab = 16000000;  // keeps every 16-bit sub-histogram counter below 65,536
 
 template <bool kVec>
 __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams p) {
-  __shared__ uint32_t hist[kTkSubHists][256];
+  __shared__ uint32_t hist[kTkSubHists][kTkHistStride];
   __shared__ uint32_t bins[256];
+  __shared__ uint32_t bin_part[4][256];
   __shared__ uint64_t cand[kTkCandCap];
   __shared__ int32_t sel[5];  // threshold key, count above, ties needed, candidates written, ties present
   __shared__ int32_t tie_scan[kTkThreads];
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int sub = (t >> 6) * 4 + (lane & 3);
+  const int sub = (t >> 6) * 16 + (lane & 15);
+  // bins 2j and 2j + 1 share dword j of a sub-histogram as its low and high 16 bits
+  auto hadd = [&](uint32_t bin) { atomicAdd(&hist[sub][bin >> 1], (bin & 1) ? 0x10000u : 1u); };
   const uint16_t* row = p.logits + int64_t(blockIdx.x) * p.stride;
   const int V = p.vocab;
   const int kk = min(p.k, V);
 
-  // f(i, key) over the row: 16-byte loads (8 logits) when rows are 16-byte aligned
-  auto for_each = [&](auto&& f) {
-    if constexpr (kVec) {
-      const int nv = V >> 3;
-      const uint4* rv = reinterpret_cast<const uint4*>(row);
-      for (int v = t; v < nv; v += kTkThreads) {
-        const uint4 w = rv[v];
-        const uint32_t u[4] = {bf16x2_keys(w.x), bf16x2_keys(w.y), bf16x2_keys(w.z), bf16x2_keys(w.w)};
+  // Rows of up to kTkResident vectors per thread are read once: their keys stay in
+  // registers (two 16-bit keys per dword) for all passes.
+  uint32_t kr[kTkResident][4];
+  const bool resident = kVec && (V >> 3) <= kTkResident * kTkThreads;
+  if (resident) {
+    const int nv = V >> 3;
+    const uint4* rv = reinterpret_cast<const uint4*>(row);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f(8 * v + 2 * e, u[e] & 0xffffu);
-          f(8 * v + 2 * e + 1, u[e] >> 16);
+    for (int j = 0; j < kTkResident; ++j) {
+      const int v = t + j * kTkThreads;
+      const uint4 w = v < nv ? rv[v] : make_uint4(0u, 0u, 0u, 0u);
+      kr[j][0] = bf16x2_keys(w.x);
+      kr[j][1] = bf16x2_keys(w.y);
+      kr[j][2] = bf16x2_keys(w.z);
+      kr[j][3] = bf16x2_keys(w.w);
+    }
+  }
+  // f(i, key) over the row: from registers, else 16-byte loads (8 logits, four in flight per
+  // thread) when rows are 16-byte aligned, else element loads
+  auto for_each = [&](auto&& f) {
+    const int nv = kVec ? V >> 3 : 0;
+    if (resident) {
+#pragma unroll
+      for (int j = 0; j < kTkResident; ++j) {
+        const int v = t + j * kTkThreads;
+        if (v < nv) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            f(8 * v + 2 * e, kr[j][e] & 0xffffu);
+            f(8 * v + 2 * e + 1, kr[j][e] >> 16);
+          }
         }
       }
-      for (int i = (nv << 3) + t; i < V; i += kTkThreads) f(i, bf16_key(row[i]));
-    } else {
-      for (int i = t; i < V; i += kTkThreads) f(i, bf16_key(row[i]));
+    } else if (kVec) {
+      constexpr int kInFlight = 4;
+      const uint4* rv = reinterpret_cast<const uint4*>(row);
+      for (int v0 = t; v0 < nv; v0 += kInFlight * kTkThreads) {
+        uint4 wv[kInFlight];
+#pragma unroll
+        for (int j = 0; j < kInFlight; ++j) {
+          const int v = v0 + j * kTkThreads;
+          if (v < nv) wv[j] = rv[v];
+        }
+#pragma unroll
+        for (int j = 0; j < kInFlight; ++j) {
+          const int v = v0 + j * kTkThreads;
+          if (v < nv) {
+            const uint32_t u[4] = {bf16x2_keys(wv[j].x), bf16x2_keys(wv[j].y), bf16x2_keys(wv[j].z),
+                                   bf16x2_keys(wv[j].w)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              f(8 * v + 2 * e, u[e] & 0xffffu);
+              f(8 * v + 2 * e + 1, u[e] >> 16);
+            }
+          }
+        }
+      }
     }
+    for (int i = (nv << 3) + t; i < V; i += kTkThreads) f(i, bf16_key(row[i]));
   };
   auto clear_hist = [&]() {
-    for (int i = t; i < kTkSubHists * 256; i += kTkThreads) (&hist[0][0])[i] = 0;
+    for (int i = t; i < kTkSubHists * kTkHistStride; i += kTkThreads) (&hist[0][0])[i] = 0;
   };
+  // bins[b] = sum over sub-histograms (each quarter of the threads sums a quarter of them)
   auto sum_hist = [&]() {
-    if (t < 256) {
+    {
+      const int b = t & 255, q = t >> 8;
       uint32_t c = 0;
-      for (int h = 0; h < kTkSubHists; ++h) c += hist[h][t];
-      bins[t] = c;
+      for (int h = q * (kTkSubHists / 4); h < (q + 1) * (kTkSubHists / 4); ++h) c += hist[h][b >> 1];
+      bin_part[q][b] = (b & 1) ? (c >> 16) : (c & 0xffffu);
+    }
+    __syncthreads();
+    if (t < 256) bins[t] = bin_part[0][t] + bin_part[1][t] + bin_part[2][t] + bin_part[3][t];
+  };
+  // The boundary bin below `base` keys counted above the histogram: the largest b with
+  // base + sum(bins[b..255]) >= kk (or 0), from suffix sums of 4 bins per lane of wave 0 and
+  // one ballot; the lane holding it stores (b, keys above b[, keys in b]).
+  auto boundary = [&](uint32_t base, int* out_bin, int* out_above, int* out_count) {
+    const uint32_t c0 = bins[4 * lane], c1 = bins[4 * lane + 1], c2 = bins[4 * lane + 2], c3 = bins[4 * lane + 3];
+    const uint32_t own = c0 + c1 + c2 + c3;
+    uint32_t suf = own;  // sum over lanes >= lane
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_down(suf, off);
+      if (lane + off < 64) suf += o;
+    }
+    const uint32_t s3 = base + suf - own + c3, s2 = s3 + c2, s1 = s2 + c1, s0 = s1 + c0;
+    const uint32_t need = uint32_t(kk);
+    const int mine = s3 >= need ? 3 : s2 >= need ? 2 : s1 >= need ? 1 : s0 >= need ? 0 : -1;
+    const uint64_t m = __ballot(mine >= 0);
+    const int hl = m ? 63 - __builtin_clzll(m) : 0;
+    if (lane == hl) {
+      const int j = mine >= 0 ? mine : 0;
+      const uint32_t sj = j == 3 ? s3 : j == 2 ? s2 : j == 1 ? s1 : s0;
+      const uint32_t cj = j == 3 ? c3 : j == 2 ? c2 : j == 1 ? c1 : c0;
+      *out_bin = 4 * lane + j;
+      *out_above = int(sj - cj);
+      if (out_count) *out_count = int(cj);
     }
   };
 
   // pass 1: high byte
   clear_hist();
   __syncthreads();
-  for_each([&](int, uint32_t key) { atomicAdd(&hist[sub][key >> 8], 1u); });
+  for_each([&](int, uint32_t key) { hadd(key >> 8); });
   __syncthreads();
   sum_hist();
   __syncthreads();
-  if (t == 0) {
-    uint32_t above = 0;
-    int hb = 255;
-    for (; hb > 0; --hb) {
-      if (above + bins[hb] >= uint32_t(kk)) break;
-      above += bins[hb];
-    }
-    sel[0] = hb;
-    sel[1] = int(above);
-  }
+  if (t < 64) boundary(0u, &sel[0], &sel[1], nullptr);
   __syncthreads();
   const uint32_t hb = uint32_t(sel[0]);
   // pass 2: low byte among keys in the boundary bin
   clear_hist();
   __syncthreads();
   for_each([&](int, uint32_t key) {
-    if ((key >> 8) == hb) atomicAdd(&hist[sub][key & 255], 1u);
+    if ((key >> 8) == hb) hadd(key & 255);
   });
   __syncthreads();
   sum_hist();
   __syncthreads();
+  if (t < 64) {
+    const uint32_t base = uint32_t(sel[1]);
+    __builtin_amdgcn_wave_barrier();
+    boundary(base, &sel[0], &sel[1], &sel[4]);  // low byte, keys above it, keys equal to it
+  }
+  __syncthreads();
   if (t == 0) {
-    uint32_t above = uint32_t(sel[1]);
-    int lb = 255;
-    for (; lb > 0; --lb) {
-      if (above + bins[lb] >= uint32_t(kk)) break;
-      above += bins[lb];
-    }
-    sel[0] = int((hb << 8) | uint32_t(lb));  // the k-th largest key
-    sel[1] = int(above);                      // keys above it
-    sel[2] = kk - int(above);                 // ties to take, lowest ids first
+    sel[0] = int((hb << 8) | uint32_t(sel[0]));  // the k-th largest key
+    sel[2] = kk - sel[1];                       // ties to take, lowest ids first
     sel[3] = 0;
-    sel[4] = int(bins[lb]);                   // keys equal to it
   }
   __syncthreads();
   const uint32_t kth = uint32_t(sel[0]);
@@ -309,7 +377,23 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
   while (n2 < n_sort) n2 <<= 1;
   for (int i = n_sort + t; i < n2; i += kTkThreads) cand[i] = 0;
   __syncthreads();
-  // bitonic sort, descending
+  if (n2 <= 64) {
+    // bitonic sort of at most 64 candidates in one wave's registers, descending
+    if (t < 64) {
+      uint64_t x = lane < n2 ? cand[lane] : 0ull;
+      for (int size = 2; size <= 64; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          const uint32_t lo = __shfl_xor(uint32_t(x), stride), hi = __shfl_xor(uint32_t(x >> 32), stride);
+          const uint64_t y = (uint64_t(hi) << 32) | lo;
+          const bool keep_max = ((lane & size) == 0) == ((lane & stride) == 0);
+          x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+        }
+      }
+      if (lane < n2) cand[lane] = x;
+    }
+    __syncthreads();
+  } else
+  // bitonic sort in LDS, descending
   for (int size = 2; size <= n2; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       for (int i = t; i < n2; i += kTkThreads) {
@@ -594,7 +678,7 @@ extern "C" int aspire_topk_candidates(const void* logits, int64_t stride, int32_
                                       int64_t vocab_start, void* values, int64_t* ids, void* stream) {
   using namespace aspire;
   ASPIRE_CHECK_ARG(rows >= 0 && vocab >= 1 && top_k >= 1 && top_k <= kMaxTopK, "need vocab >= 1, 1 <= top_k <= 1024");
-  ASPIRE_CHECK_ARG(vocab <= (1 << 30) && stride >= vocab, "bad vocab / row stride");
+  ASPIRE_CHECK_ARG(vocab <= kTkMaxVocab && stride >= vocab, "need vocab <= 16,000,000 and stride >= vocab");
   if (rows == 0) return ASPIRE_OK;
   ASPIRE_CHECK_ARG(logits && values && ids, "null pointer");
   TopKParams p{static_cast<const uint16_t*>(logits), stride, vocab, top_k, vocab_start,

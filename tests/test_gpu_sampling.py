@@ -19,8 +19,11 @@ MARGIN = 1e-5
 
 
 @pytest.mark.parametrize("rows,vocab,k,start", [(208, 151936, 50, 0), (33, 1000, 64, 7), (5, 37, 50, 151936),
-                                                 (4, 4096, 1024, 0)])
+                                                 (4, 4096, 1024, 0), (2, 155648, 64, 0), (3, 262152, 50, 0),
+                                                 (2, 262151, 50, 0)])
 def test_topk_candidates_exact(gpu, rows, vocab, k, start):
+    """Rows kept in registers (up to 155,648 logits, the largest filling every register slot),
+    rows streamed with 16-byte loads (262,152) and with element loads (an odd row length)."""
     say("topk candidates", rows, vocab, k)
     g = torch.Generator().manual_seed(vocab + k)
     # coarse logits: many equal bf16 values, so the tie rule decides the boundary
@@ -39,8 +42,8 @@ def test_topk_candidates_paths(gpu, case):
     key >= the k-th), rows of one repeated value and rows where the boundary value repeats
     thousands of times (ties overflow the candidate buffer: the id-ordered tie ranking), and a
     view whose rows start 2 bytes past a 16-byte boundary (2-byte loads); and rows whose largest
-    keys are a few outliers, so the histogram from one bin below the maximum's bin holds fewer
-    than k keys and is redone over every bin."""
+    keys are a few outliers far above the rest, so the boundary lies many bins below the
+    maximum's."""
     say("topk candidates path", case)
     g = torch.Generator().manual_seed(11)
     rows, vocab, k = 6, 20016, 100
