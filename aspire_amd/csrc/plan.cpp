@@ -28,6 +28,13 @@ namespace aspire {
 namespace {
 
 constexpr int kMinPagesPerWave = 8;
+// Relative wave time of one page of a per-head (direct) item against one page staged for a
+// workgroup's heads, as stream-K cost units.
+#ifndef ASPIRE_DIRECT_PAGE_COST
+#define ASPIRE_DIRECT_PAGE_COST 11
+#endif
+constexpr int64_t kDirectPageCost = ASPIRE_DIRECT_PAGE_COST;
+constexpr int64_t kSharedPageCost = 8;
 
 struct Segment {
   int32_t q_start, q_len, kv_len, list_base, npages, bg, rows;
@@ -35,8 +42,13 @@ struct Segment {
   int32_t direct;  // kItemDirect for rows whose heads read different lists
 };
 
+struct Piece {
+  int64_t slot, pb, pe;  // slot and the segment's pages [pb, pe) it streams
+};
+
 struct Scratch {
   std::vector<Segment> segs[3];
+  std::vector<Piece> pieces;
   std::vector<int32_t> start, pages;
   std::vector<std::pair<int32_t, WorkItem>> items;
   std::vector<MergeItem> merges;
@@ -197,12 +209,23 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
 
   for (int c = 0; c < 3; ++c) {
     const auto& segs = sc.segs[c];
+    int64_t T_pages = 0;
+    bool any_direct = false, any_shared = false;
+    for (const auto& s : segs) {
+      T_pages += s.npages;
+      if (s.npages > 0) (s.direct ? any_direct : any_shared) = true;
+    }
+    // Stream-K positions are in cost units: a page of a per-head (direct) segment costs
+    // more wave time than a page staged once for the workgroup's heads, so a class that
+    // holds both splits its total cost, not its page count, evenly over the slots.
+    const bool weighted = any_direct && any_shared;
+    const int64_t w_direct = weighted ? kDirectPageCost : 1, w_shared = weighted ? kSharedPageCost : 1;
     int64_t T = 0;
-    for (const auto& s : segs) T += s.npages;
-    total_pages += T * hpu;
+    for (const auto& s : segs) T += int64_t(s.npages) * (s.direct ? w_direct : w_shared);
+    total_pages += T_pages * hpu;
     const int64_t slots = W / hpu;
     // Slots actually used: enough that each streams >= kMinPagesPerWave pages.
-    int64_t s_eff = std::max<int64_t>(1, std::min<int64_t>(slots, T / kMinPagesPerWave));
+    int64_t s_eff = std::max<int64_t>(1, std::min<int64_t>(slots, T_pages / kMinPagesPerWave));
     // Shrink until the split pieces' partial rows fit the float workspace.
     for (;;) {
       sc.items.clear();
@@ -220,28 +243,37 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
           }
           continue;
         }
-        const int64_t a = seg_off, e = seg_off + s.npages;
-        // slot containing global page a: largest j with floor(j*T/s_eff) <= a
-        int64_t j_lo = (a * s_eff) / T;
-        while (j_lo > 0 && (j_lo * T) / s_eff > a) --j_lo;
-        while (j_lo + 1 < s_eff && ((j_lo + 1) * T) / s_eff <= a) ++j_lo;
-        int64_t j_hi = ((e - 1) * s_eff) / T;
-        while (j_hi > 0 && (j_hi * T) / s_eff > e - 1) --j_hi;
-        while (j_hi + 1 < s_eff && ((j_hi + 1) * T) / s_eff <= e - 1) ++j_hi;
-        const int pieces = static_cast<int>(j_hi - j_lo + 1);
+        // Page p of the segment sits at cost position a + p * wt and belongs to the slot
+        // holding that position: slot j holds positions [floor(j*T/s_eff), floor((j+1)*T/s_eff)).
+        const int64_t wt = s.direct ? w_direct : w_shared;
+        const int64_t a = seg_off, e = seg_off + int64_t(s.npages) * wt;
+        auto slot_of = [&](int64_t x) {  // largest j with floor(j*T/s_eff) <= x
+          int64_t j = (x * s_eff) / T;
+          while (j > 0 && (j * T) / s_eff > x) --j;
+          while (j + 1 < s_eff && ((j + 1) * T) / s_eff <= x) ++j;
+          return j;
+        };
+        auto first_page_at = [&](int64_t x) {  // first page whose position is >= x
+          return x <= a ? int64_t(0) : std::min<int64_t>(s.npages, (x - a + wt - 1) / wt);
+        };
+        const int64_t j_lo = slot_of(a), j_hi = slot_of(e - wt);
+        sc.pieces.clear();
+        for (int64_t j = j_lo; j <= j_hi; ++j) {
+          const int64_t pb = first_page_at((j * T) / s_eff), pe = j == j_hi ? s.npages : first_page_at(((j + 1) * T) / s_eff);
+          if (pe > pb) sc.pieces.push_back({j, pb, pe});
+        }
+        const int pieces = static_cast<int>(sc.pieces.size());
         // partial rows: head gg's pieces are contiguous, first[gg] + k * rows
         const int64_t first = pr;
         if (pieces > 1) pr += int64_t(hpu) * pieces * s.rows;
-        for (int64_t j = j_lo; j <= j_hi; ++j) {
-          const int64_t wb = std::max(a, (j * T) / s_eff);
-          const int64_t we = std::min(e, ((j + 1) * T) / s_eff);
-          const int64_t k = j - j_lo;
+        for (int k = 0; k < pieces; ++k) {
+          const Piece& pc = sc.pieces[k];
           for (int gg = 0; gg < hpu; ++gg) {
             const int64_t prow = pieces > 1 ? first + (int64_t(gg) * pieces + k) * s.rows : -1;
             const int32_t base = s.seg0 >= 0 ? seg_start[s.seg0 + gg] : s.list_base;
-            WorkItem it{s.q_start, s.q_len | s.direct, s.kv_len, base, static_cast<int32_t>(wb - a),
-                        static_cast<int32_t>(we - a), s.bg + gg, static_cast<int32_t>(prow)};
-            sc.items.emplace_back(static_cast<int32_t>(((j + rot) % slots) * hpu + gg), it);
+            WorkItem it{s.q_start, s.q_len | s.direct, s.kv_len, base, static_cast<int32_t>(pc.pb),
+                        static_cast<int32_t>(pc.pe), s.bg + gg, static_cast<int32_t>(prow)};
+            sc.items.emplace_back(static_cast<int32_t>(((pc.slot + rot) % slots) * hpu + gg), it);
           }
         }
         if (pieces > 1) {
