@@ -28,13 +28,18 @@ namespace aspire {
 namespace {
 
 constexpr int kMinPagesPerWave = 8;
-// Relative wave time of one page of a per-head (direct) item against one page staged for a
-// workgroup's heads, as stream-K cost units.
+// Stream-K cost units: measured wave time of one page-head of a 1- or 2-tile item staged for
+// the workgroup's heads (8), of a 1- or 2-tile item reading its own head's list (direct: 11),
+// and of a 3-tile item (10).
 #ifndef ASPIRE_DIRECT_PAGE_COST
 #define ASPIRE_DIRECT_PAGE_COST 11
 #endif
+#ifndef ASPIRE_THREE_TILE_PAGE_COST
+#define ASPIRE_THREE_TILE_PAGE_COST 10
+#endif
 constexpr int64_t kDirectPageCost = ASPIRE_DIRECT_PAGE_COST;
 constexpr int64_t kSharedPageCost = 8;
+constexpr int64_t kThreeTilePageCost = ASPIRE_THREE_TILE_PAGE_COST;
 
 struct Segment {
   int32_t q_start, q_len, kv_len, list_base, npages, bg, rows;
@@ -49,6 +54,7 @@ struct Piece {
 struct Scratch {
   std::vector<Segment> segs[3];
   std::vector<Piece> pieces;
+  std::vector<std::pair<int32_t, WorkItem>> citems[3];
   std::vector<int32_t> start, pages;
   std::vector<std::pair<int32_t, WorkItem>> items;
   std::vector<MergeItem> merges;
@@ -201,51 +207,47 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
   int64_t partial_rows = 0;
   int64_t total_pages = 0;
   int num_items[3] = {0, 0, 0};
-  // One kernel launch runs every class (each wave takes its class-1 items,
-  // then class 2, then class 3), so a class using fewer slots than there are
-  // starts where the previous class's slots ended: small classes land on
-  // different waves instead of all on the first ones.
-  int64_t rot = 0;
-
-  for (int c = 0; c < 3; ++c) {
-    const auto& segs = sc.segs[c];
-    int64_t T_pages = 0;
-    bool any_direct = false, any_shared = false;
-    for (const auto& s : segs) {
+  // One kernel launch runs every class: each wave takes its class-1 items, then its class-2,
+  // then its class-3 items. The classes are planned as one stream-K sequence in cost units
+  // (class by class, segments in row order), so a slot streams one contiguous range of that
+  // sequence and a long row is split about as often as its share of the whole launch needs,
+  // not once per slot of its class.
+  auto page_cost = [&](int c, bool direct) -> int64_t {
+    if (c == 2) return kThreeTilePageCost;
+    return direct ? kDirectPageCost : kSharedPageCost;
+  };
+  int64_t T = 0, T_pages = 0;
+  for (int c = 0; c < 3; ++c)
+    for (const auto& s : sc.segs[c]) {
+      T += int64_t(s.npages) * page_cost(c, s.direct != 0);
       T_pages += s.npages;
-      if (s.npages > 0) (s.direct ? any_direct : any_shared) = true;
     }
-    // Stream-K positions are in cost units: a page of a per-head (direct) segment costs
-    // more wave time than a page staged once for the workgroup's heads, so a class that
-    // holds both splits its total cost, not its page count, evenly over the slots.
-    const bool weighted = any_direct && any_shared;
-    const int64_t w_direct = weighted ? kDirectPageCost : 1, w_shared = weighted ? kSharedPageCost : 1;
-    int64_t T = 0;
-    for (const auto& s : segs) T += int64_t(s.npages) * (s.direct ? w_direct : w_shared);
-    total_pages += T_pages * hpu;
-    const int64_t slots = W / hpu;
-    // Slots actually used: enough that each streams >= kMinPagesPerWave pages.
-    int64_t s_eff = std::max<int64_t>(1, std::min<int64_t>(slots, T_pages / kMinPagesPerWave));
-    // Shrink until the split pieces' partial rows fit the float workspace.
-    for (;;) {
-      sc.items.clear();
-      int64_t pr = partial_rows;
-      size_t merges_before = sc.merges.size();
-      int64_t seg_off = 0;
-      int zero_rr = 0;
-      for (const auto& s : segs) {
+  total_pages = T_pages * hpu;
+  const int64_t slots = W / hpu;
+  // Slots actually used: enough that each streams >= kMinPagesPerWave pages.
+  int64_t s_eff = std::max<int64_t>(1, std::min<int64_t>(slots, T_pages / kMinPagesPerWave));
+  // Shrink until the split pieces' partial rows fit the float workspace.
+  for (;;) {
+    for (auto& v : sc.citems) v.clear();
+    sc.merges.clear();
+    int64_t pr = 0;
+    int64_t seg_off = 0;
+    int zero_rr = 0;
+    for (int c = 0; c < 3; ++c) {
+      auto& out = sc.citems[c];
+      for (const auto& s : sc.segs[c]) {
         if (s.npages == 0) {
-          const int64_t slot = (zero_rr++ % s_eff + rot) % slots;
+          const int64_t slot = zero_rr++ % s_eff;
           for (int gg = 0; gg < hpu; ++gg) {
             const int32_t base = s.seg0 >= 0 ? seg_start[s.seg0 + gg] : s.list_base;
             WorkItem it{s.q_start, s.q_len | s.direct, s.kv_len, base, 0, 0, s.bg + gg, -1};
-            sc.items.emplace_back(static_cast<int32_t>(slot * hpu + gg), it);
+            out.emplace_back(static_cast<int32_t>(slot * hpu + gg), it);
           }
           continue;
         }
         // Page p of the segment sits at cost position a + p * wt and belongs to the slot
         // holding that position: slot j holds positions [floor(j*T/s_eff), floor((j+1)*T/s_eff)).
-        const int64_t wt = s.direct ? w_direct : w_shared;
+        const int64_t wt = page_cost(c, s.direct != 0);
         const int64_t a = seg_off, e = seg_off + int64_t(s.npages) * wt;
         auto slot_of = [&](int64_t x) {  // largest j with floor(j*T/s_eff) <= x
           int64_t j = (x * s_eff) / T;
@@ -259,7 +261,8 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
         const int64_t j_lo = slot_of(a), j_hi = slot_of(e - wt);
         sc.pieces.clear();
         for (int64_t j = j_lo; j <= j_hi; ++j) {
-          const int64_t pb = first_page_at((j * T) / s_eff), pe = j == j_hi ? s.npages : first_page_at(((j + 1) * T) / s_eff);
+          const int64_t pb = first_page_at((j * T) / s_eff);
+          const int64_t pe = j == j_hi ? s.npages : first_page_at(((j + 1) * T) / s_eff);
           if (pe > pb) sc.pieces.push_back({j, pb, pe});
         }
         const int pieces = static_cast<int>(sc.pieces.size());
@@ -273,7 +276,7 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
             const int32_t base = s.seg0 >= 0 ? seg_start[s.seg0 + gg] : s.list_base;
             WorkItem it{s.q_start, s.q_len | s.direct, s.kv_len, base, static_cast<int32_t>(pc.pb),
                         static_cast<int32_t>(pc.pe), s.bg + gg, static_cast<int32_t>(prow)};
-            sc.items.emplace_back(static_cast<int32_t>(((pc.slot + rot) % slots) * hpu + gg), it);
+            out.emplace_back(static_cast<int32_t>(pc.slot * hpu + gg), it);
           }
         }
         if (pieces > 1) {
@@ -289,30 +292,31 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
         }
         seg_off = e;
       }
-      if (pr <= L.partial_rows_cap || s_eff == 1) {
-        if (pr > L.partial_rows_cap)
-          return fail(ASPIRE_ERR_CAPACITY, "aspire_plan_build: float workspace too small");
-        partial_rows = pr;
-        break;
-      }
-      sc.merges.resize(merges_before);
-      s_eff = std::max<int64_t>(1, s_eff / 2);
     }
-    if (!segs.empty()) rot = (rot + s_eff) % slots;
-    if (static_cast<int64_t>(sc.items.size()) > L.max_items) {
-      set_error("aspire_plan_build: class %d needs %zu work items, capacity %d", c,
-                sc.items.size(), L.max_items);
+    if (pr <= L.partial_rows_cap || s_eff == 1) {
+      if (pr > L.partial_rows_cap)
+        return fail(ASPIRE_ERR_CAPACITY, "aspire_plan_build: float workspace too small");
+      partial_rows = pr;
+      break;
+    }
+    s_eff = std::max<int64_t>(1, s_eff / 2);
+  }
+  for (int c = 0; c < 3; ++c) {
+    const auto& citems = sc.citems[c];
+    if (static_cast<int64_t>(citems.size()) > L.max_items) {
+      set_error("aspire_plan_build: class %d needs %zu work items, capacity %d", c, citems.size(),
+                L.max_items);
       return ASPIRE_ERR_CAPACITY;
     }
     // CSR by wave (stable: keeps each wave's pieces in page order).
     sc.counts.assign(W + 1, 0);
-    for (const auto& pi : sc.items) sc.counts[pi.first + 1]++;
+    for (const auto& pi : citems) sc.counts[pi.first + 1]++;
     for (int w = 0; w < W; ++w) sc.counts[w + 1] += sc.counts[w];
     int32_t* indptr = buf + off.indptr[c];
     std::memcpy(indptr, sc.counts.data(), sizeof(int32_t) * (W + 1));
     WorkItem* items = reinterpret_cast<WorkItem*>(buf + off.items[c]);
-    for (const auto& pi : sc.items) items[sc.counts[pi.first]++] = pi.second;
-    num_items[c] = static_cast<int>(sc.items.size());
+    for (const auto& pi : citems) items[sc.counts[pi.first]++] = pi.second;
+    num_items[c] = static_cast<int>(citems.size());
   }
   if (static_cast<int64_t>(sc.merges.size()) > L.max_merge) {
     set_error("aspire_plan_build: %zu merge items, capacity %d", sc.merges.size(), L.max_merge);

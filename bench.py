@@ -72,8 +72,9 @@ def parse():
                          "layer at --draft-frac")
     ap.add_argument("--draft-frac", type=float, default=0.5, help="config 4: fraction of drafting rows")
     ap.add_argument("--class-mask", type=int, default=0,
-                    help="config 4: time only the attention launch of these row-tile classes (bit c-1 for class c: "
-                         "<=16, <=32, <=48 query rows), no merge; value counts their KV bytes (for per-class counters)")
+                    help="config 4: plan only the rows of these row-tile classes (bit c-1 for class c: <=16, <=32, "
+                         "<=48 query rows) and time their attention launch, no merge; value counts their KV bytes "
+                         "(for per-class counters)")
     ap.add_argument("--waves-per-cu", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed CPU-baseline runs per config (after 2 warm-ups)")
@@ -153,6 +154,19 @@ def graph_timed(fn, steps, stream, reps=20, warm=2):
     ms = timed(g.replay, steps, stream) / reps
     del g
     return ms
+
+
+def plan_rows_subset(w, st, keep):
+    """Re-plan ``w`` over the rows of ``st`` where ``keep`` holds (the other rows get no queries):
+    the plan spreads every class over all waves in one cost-ordered sequence, so a class is
+    timed alone by planning its rows alone, not by masking classes out of a joint plan."""
+    from aspire_amd.workloads import PAGE
+
+    qo_full = st.qo_indptr_host.numpy()
+    qo = qo_full.copy()  # same length (padding entries keep the bucket's end)
+    qo[1 : st.batch + 1] = np.cumsum(np.where(keep, st.q_len, 0))
+    qo = torch.from_numpy(qo.astype(np.int32)).to(st.q.device)
+    w.plan(qo, st.kv_indptr, st.kv_indices, st.last_page_len, st.hq, st.hkv, 128, PAGE, causal=True)
 
 
 def attention_only(w, q, cache, out, class_mask=None):
@@ -257,10 +271,11 @@ def main():
             w.run(step.q, cache, out=out, page_scores=selector.page_scores)
             selector.select(npg, step.block_table)
     elif args.config == 4 and args.class_mask:
-        run_step = attention_only(w, step.q, cache, out, class_mask=args.class_mask)
         rows = step.q_len * (step.hq // step.hkv)
         cls = np.where(rows <= 16, 0, np.where(rows <= 32, 1, 2))
         keep = np.array([(args.class_mask >> c) & 1 for c in range(3)], dtype=bool)[cls]
+        plan_rows_subset(w, step, keep)
+        run_step = attention_only(w, step.q, cache, out)
         kvl = step.kv_len_host.numpy()[: step.batch].astype(np.int64)
         nbytes = {"kv": int(kvl[keep].sum()) * step.hkv * 128 * 4, "qo": 0, "indices": 0}
         nbytes["total"] = nbytes["kv"]
@@ -282,7 +297,7 @@ def main():
     value = nbytes["total"] / (ms * 1e-3) / 1e9
 
     # dominant kernel alone: mixed attention (no merge), same plan, same stream
-    attn = attention_only(w, step.q, cache, out, class_mask=(args.class_mask or None) if args.config == 4 else None)
+    attn = attention_only(w, step.q, cache, out)
     for _ in range(3):
         attn()
     attn_ms, attn_per = timed_steps(attn, args.steps, stream)
@@ -329,7 +344,8 @@ def main():
                     "attention + split-KV merge")
         metric = f"long-context layer HBM GB/s (DS-Llama-8B shape, B=16, ctx U[64k,128k], f={args.draft_frac})"
         if args.class_mask:
-            workload += f"; attention launch of row-tile class mask {args.class_mask} only (KV bytes of those rows)"
+            workload += (f"; only the rows of row-tile class mask {args.class_mask}, planned alone: attention "
+                         "launch, KV bytes of those rows")
             metric += f", class mask {args.class_mask}"
     line = {
         "metric": metric,
@@ -650,15 +666,16 @@ def measure_config4(steps, waves_per_cu, fracs=(0.0, 0.25, 0.5, 0.75, 1.0)):
         nb = st.algorithmic_bytes(include_append=False)["total"]
         info = w.plan_info
         gbs = nb / (ms * 1e-3) / 1e9
-        # each row-tile class alone (rows = q_len * group: <=16, <=32, <=48)
+        # each row-tile class alone (rows = q_len * group: <=16, <=32, <=48), planned alone
         rows = st.q_len * (st.hq // st.hkv)
         cls = np.where(rows <= 16, 0, np.where(rows <= 32, 1, 2))
         kvl = st.kv_len_host.numpy()[: st.batch].astype(np.int64)
         per_class = {}
         for c in range(3):
-            if info.num_items[c] == 0:
+            if not (cls == c).any():
                 continue
-            fn_c = attention_only(w, st.q, st.cache, out, class_mask=1 << c)
+            plan_rows_subset(w, st, cls == c)
+            fn_c = attention_only(w, st.q, st.cache, out)
             fn_c()
             us_c = timed(fn_c, steps, stream) * 1e3
             nb_c = int(kvl[cls == c].sum()) * st.hkv * 128 * 4

@@ -300,11 +300,11 @@ def test_rejects_gqa_group_wider_than_three_tiles():
     plan(lay, qo, kvp, kvl, 48, 1)
 
 
-def test_merge_row_ranges_config3_layer():
+def test_config3_layer_cost_balance():
     """A config-3 mixed layer (64 rows, contexts U[8k, 32k], per-head top-128 draft lists, verify
-    q_len U{2..9}) on 256 CUs: the two long q_len-9 rows of the 3-tile class are split into
-    60-69 pieces, and their 36-row merges come as row ranges of 12 rows, so that four lane groups
-    share each row's pieces; items of at most 8 pieces stay whole."""
+    q_len U{2..9}) on 256 CUs: the three row-tile classes form one stream-K sequence in cost
+    units (8 per staged 1-/2-tile page, 11 per per-head page, 10 per 3-tile page), so every slot
+    streams the mean cost to within one page, and no merge needs more than one round of loads."""
     from aspire_amd.workloads import PAGE, config3_rows
 
     ctx, ql, dr = config3_rows(seed=0)
@@ -322,8 +322,33 @@ def test_merge_row_ranges_config3_layer():
     lay = layout(num_cus=256, waves_per_cu=4)
     buf, info = plan_segments(lay, qo, starts, pages, kvl, hq, hkv)
     check_cover(lay, buf, info, qo, None, np.array(kvl), hq, hkv, per_head=True, seg_start=np.array(starts))
+    classes, merges = decode(lay, buf, info)
+    hpu = int(buf[4])
+    assert hpu == hkv
+    cost = np.zeros(lay.num_waves)
+    for c, (ip, it) in enumerate(classes):
+        for w in range(lay.num_waves):
+            for row in it[ip[w] : ip[w + 1]]:
+                direct = (int(row[1]) & DIRECT) != 0
+                cost[w] += (int(row[5]) - int(row[4])) * (10 if c == 2 else 11 if direct else 8)
+    slot_cost = cost[::hpu]
+    assert slot_cost.max() - slot_cost.min() <= 2 * 11
+    assert (merges[:, 4] <= 8).all()
+
+
+def test_merge_row_ranges_lone_long_row():
+    """One 131,072-token verify row with q_len 9 at GQA 4 (36 rows, 3 tiles) beside a short draft
+    row: the long row streams over every slot, and its 36-row merges come as row ranges of 12 rows,
+    so that four lane groups share each row's pieces."""
+    hq, hkv = 32, 8
+    ql = np.array([9, 1])
+    kvl = np.array([131072, 300])
+    pages = (kvl + 15) // 16
+    qo = np.concatenate([[0], np.cumsum(ql)])
+    kvp = np.concatenate([[0], np.cumsum(pages)])
+    lay = layout(num_cus=256, waves_per_cu=4)
+    buf, info = plan(lay, qo, kvp, kvl, hq, hkv)
+    check_cover(lay, buf, info, qo, kvp, kvl, hq, hkv)
     _, merges = decode(lay, buf, info)
-    long = merges[merges[:, 4] > 16]
-    assert len(long) and (long[:, 7] <= 12).all() and (long[:, 5] == 36).any()
-    short = merges[merges[:, 4] <= 8]
-    assert (short[:, 6] == 0).all() and (short[:, 7] == short[:, 5]).all()
+    long = merges[merges[:, 5] == 36]
+    assert len(long) and (long[:, 4] > 16).all() and (long[:, 7] == 12).all()
