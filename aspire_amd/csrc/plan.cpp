@@ -28,14 +28,14 @@ namespace aspire {
 namespace {
 
 constexpr int kMinPagesPerWave = 8;
-// Stream-K cost units: measured wave time of one page-head of a 1- or 2-tile item staged for
-// the workgroup's heads (8), of a 1- or 2-tile item reading its own head's list (direct: 11),
-// and of a 3-tile item (10).
+// Stream-K cost units of one page-head: a 1- or 2-tile item staged for the workgroup's heads
+// (8), a 1- or 2-tile item reading its own head's list (direct: 12) and a 3-tile item (9),
+// chosen by sweeping them on mixed workloads (configs 3 and 4 at every draft fraction).
 #ifndef ASPIRE_DIRECT_PAGE_COST
-#define ASPIRE_DIRECT_PAGE_COST 11
+#define ASPIRE_DIRECT_PAGE_COST 12
 #endif
 #ifndef ASPIRE_THREE_TILE_PAGE_COST
-#define ASPIRE_THREE_TILE_PAGE_COST 10
+#define ASPIRE_THREE_TILE_PAGE_COST 9
 #endif
 constexpr int64_t kDirectPageCost = ASPIRE_DIRECT_PAGE_COST;
 constexpr int64_t kSharedPageCost = 8;
