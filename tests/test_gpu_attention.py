@@ -222,21 +222,33 @@ def test_segment_plan_shared_and_per_head_rows(gpu, wpc):
     assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
 
 
-@pytest.mark.parametrize("kind", ["first_last_compact", "last_token"])
-def test_logits_dump(gpu, kind):
-    say("dump", kind)
-    step = build_step(hq=16, hkv=8, ctx_len=[500, 77, 1000], q_len=[5, 1, 3], is_draft=[0, 0, 0], draft_budget=0,
-                      seed=12, device=gpu)
-    B, H = step.batch, 16
-    stride = 1024
+@pytest.mark.parametrize("kind,dtype,shape", [
+    ("first_last_compact", torch.float16, "small"), ("last_token", torch.float16, "small"),
+    ("first_last_compact", torch.float32, "long"), ("last_token", torch.float16, "long"),
+    ("last_token", torch.float16, "odd_stride")])
+def test_logits_dump(gpu, kind, dtype, shape):
+    """Dump entries against the oracle's, fp16 and fp32: 8- or 16-byte stores of a lane's 4 keys
+    when the row stride is a multiple of 4 (one store per key otherwise, and on a partial last
+    group). The long case (GQA 4, contexts of 4,099 / 535 / 9,000 tokens, a single-query row
+    beside 5- and 9-token rows of 2 and 3 tiles) splits rows into many pieces."""
+    say("dump", kind, dtype, shape)
+    if shape == "long":
+        step = build_step(hq=32, hkv=8, ctx_len=[4099, 535, 9000], q_len=[1, 5, 9], is_draft=[0, 0, 0],
+                          draft_budget=0, seed=21, device=gpu)
+        H, stride = 32, 9216
+    else:
+        step = build_step(hq=16, hkv=8, ctx_len=[500, 77, 1000], q_len=[5, 1, 3], is_draft=[0, 0, 0],
+                          draft_budget=0, seed=12, device=gpu)
+        H, stride = 16, 1024 if shape == "small" else 1023
+    B = step.batch
     slots = 2 if kind == "first_last_compact" else 1
-    args = build_holistic_dump_jit_args(torch.bfloat16, 128, dump_kind=kind, dump_buffer_dtype=torch.float16)
+    args = build_holistic_dump_jit_args(torch.bfloat16, 128, dump_kind=kind, dump_buffer_dtype=dtype)
     w = make_wrapper(gpu, jit_args=args)
     plan(w, step)
-    dump = torch.full((B * H * slots * stride,), float("-inf"), dtype=torch.float16, device=gpu)
+    dump = torch.full((B * H * slots * stride,), float("-inf"), dtype=dtype, device=gpu)
     out, lse = w.run(step.q, step.cache, dump, H, stride, return_lse=True)
     torch.cuda.synchronize()
-    ref_dump = torch.full((B * H * slots * stride,), float("-inf"), dtype=torch.float16)
+    ref_dump = torch.full((B * H * slots * stride,), float("-inf"), dtype=dtype)
     ref_out, ref_lse = oracle(step, step.cache, dump=DumpSpec(buffer=ref_dump, kind=kind.replace("_compact", ""),
                                                                 num_heads=H, kv_stride=stride))
     check_rows(step, out, lse, ref_out, ref_lse)
