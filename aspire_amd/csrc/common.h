@@ -216,21 +216,28 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 // Writes the page-list entry (kv_indptr[b] + ps / page) and the slot; false
 // when the reference skips the token (no row, negative position, empty row,
 // or past the row's length).
+// Last i in [0, n) with a[i] <= x for a non-decreasing a, or -1; wave-uniform. Every lane of
+// the wave must call it with the same arguments: lanes load 64 consecutive entries per round
+// trip and one ballot finds the boundary (a binary search would chain ~log2(n) dependent loads).
+__device__ __forceinline__ int wave_last_le(const int32_t* a, int n, int x) {
+  const int lane = threadIdx.x & 63;
+  int found = -1;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + lane;
+    const uint64_t m = __ballot(i < n && a[i] <= x);  // a prefix of the chunk's lanes
+    if (m) found = base + 63 - __builtin_clzll(m);
+    if (m != ~uint64_t(0)) break;  // an entry above x, or the array's end, is in this chunk
+  }
+  return __builtin_amdgcn_readfirstlane(found);
+}
+
+// Called by every lane of the wave (wave_last_le).
 __device__ __forceinline__ bool append_locate(const int32_t* append_indptr, int num_seq, const int32_t* kv_indptr,
                                               const int32_t* last_page_len, int page_size, int tok, int& entry,
                                               int& slot) {
   // last b in [0, num_seq) with append_indptr[b] <= tok (indptr is
   // non-decreasing, so an empty row never shadows the row that owns tok)
-  int lo = 0, hi = num_seq - 1, b = -1;
-  while (lo <= hi) {
-    const int mid = (lo + hi) >> 1;
-    if (append_indptr[mid] <= tok) {
-      b = mid;
-      lo = mid + 1;
-    } else {
-      hi = mid - 1;
-    }
-  }
+  const int b = wave_last_le(append_indptr, num_seq, tok);
   if (b < 0) return false;
   const int end = append_indptr[b + 1];
   if (tok >= end) return false;  // covered by no row: default position -1

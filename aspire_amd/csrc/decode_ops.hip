@@ -34,6 +34,14 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(uint16_t* x,
   uint4* xr = reinterpret_cast<uint4*>(x + int64_t(r) * x_stride);
   const uint4* dr = delta ? reinterpret_cast<const uint4*>(delta + int64_t(r) * d_stride) : nullptr;
   const int chunks = dim / 8;
+  // the weight is requested with the row (not after the reduction's barrier)
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4 wv[kNormMaxChunks];
+#pragma unroll
+  for (int c = 0; c < kNormMaxChunks; ++c) {
+    const int i = threadIdx.x + c * kNormThreads;
+    if (i < chunks) wv[c] = wr[i];
+  }
   float v[kNormMaxChunks][8];
   float ss = 0.f;
 #pragma unroll
@@ -73,13 +81,12 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(uint16_t* x,
 #pragma unroll
   for (int k = 0; k < kNormThreads / 64; ++k) tot += partial[k];
   const float rs = 1.f / sqrtf(tot / float(dim) + eps);
-  const uint4* wr = reinterpret_cast<const uint4*>(w);
   uint4* orow = reinterpret_cast<uint4*>(out + int64_t(r) * o_stride);
 #pragma unroll
   for (int c = 0; c < kNormMaxChunks; ++c) {
     const int i = threadIdx.x + c * kNormThreads;
     if (i < chunks) {
-      const uint4 g = wr[i];
+      const uint4 g = wv[c];
       const uint32_t gw[8] = {g.x, g.x, g.y, g.y, g.z, g.z, g.w, g.w};
       float o[8];
 #pragma unroll

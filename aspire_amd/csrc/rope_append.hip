@@ -69,16 +69,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(RopeParams p) 
   // rope position: row b of indptr owns tok (last b with indptr[b] <= tok < indptr[b + 1])
   int pos = -1;
   {
-    int lo = 0, hi = p.num_rows - 1, b = -1;
-    while (lo <= hi) {
-      const int mid = (lo + hi) >> 1;
-      if (p.indptr[mid] <= tok) {
-        b = mid;
-        lo = mid + 1;
-      } else {
-        hi = mid - 1;
-      }
-    }
+    const int b = wave_last_le(p.indptr, p.num_rows, tok);
     if (b >= 0 && tok < p.indptr[b + 1]) pos = p.offsets[b] + tok - p.indptr[b];
   }
   pos = wave_uniform(pos);

@@ -162,12 +162,28 @@ def test_small_decode_step_matches_oracle(gpu, shape):
     for layer in range(step.shape.n_layer):
         qg, qr = cap[f"q{layer}"].float().cpu(), ref[f"q{layer}"].float()
         assert (qg - qr).abs().max() <= 0.05 * qr.abs().max(), f"layer {layer} q"
+    # The page scores are the key-mean epilogue of the GPU's own refresh-layer q and cache: max over
+    # the group's heads of q . mean(k) per page, in fp32 on the CPU from the same inputs.
+    G = step.shape.n_head // H
+    q2 = cap["q2"].float().cpu()
+    kc = step.caches[2].float().cpu()
+    qo = np.concatenate([[0], np.cumsum(ql)])
+    for b in np.flatnonzero(dr):
+        for g in range(H):
+            n = int(n_pages[b])
+            want = torch.empty(n)
+            for pg in range(n):
+                kmean = kc[int(table[b][pg]), 0, : min(16, int(ctx[b]) - 16 * pg), g].mean(0)
+                want[pg] = (q2[int(qo[b]), g * G : (g + 1) * G] @ kmean).max()
+            assert torch.allclose(scores[b * H + g, :n], want, rtol=1e-3, atol=1e-3)
+    # Against the oracle's whole step: its q differs from the GPU's by the roundings of two layers
+    # (held to 5% of the largest |q| above), and so do the scores.
     ps_ref = ref["page_scores"]
     for b in np.flatnonzero(dr):
         for g in range(H):
             s = b * H + g
             n = int(n_pages[b])
-            assert torch.allclose(scores[s, :n], ps_ref[s, :n], rtol=5e-2, atol=5e-2)
+            assert (scores[s, :n] - ps_ref[s, :n]).abs().max() <= 0.05 * ps_ref[s, :n].abs().max()
     lg, lr = step.logits.float().cpu(), ref["logits"].float()
     assert torch.isfinite(lg).all()
     assert (lg - lr).abs().max() <= 0.05 * lr.abs().max()
