@@ -4,9 +4,11 @@
 //   lower id. One 1024-thread workgroup per row, 16-byte loads; rows of up to 155,648 logits
 //   are read once and kept in registers as keys. Radix select on 16-bit order-preserving keys
 //   of the bf16 logits: a histogram of the high byte, then of the low byte among the boundary
-//   bin, gives the k-th key exactly (each boundary from suffix sums in one wave); one pass
-//   collects every key at or above it and a bitonic sort (in one wave's registers up to 64
-//   candidates, else in LDS) orders them (ties by id), so the first top_k are the answer.
+//   bin, gives the k-th key exactly (each boundary from suffix sums in one wave); every key at
+//   or above it is collected (for register-held rows from the keys of the boundary bin and
+//   above, copied once into per-thread LDS regions; else by a pass over the row) and a bitonic
+//   sort (in one wave's registers up to 64 candidates, else in LDS) orders them (ties by id),
+//   so the first top_k are the answer.
 //   When the boundary key repeats so often that the candidates overflow LDS, an ordered pass
 //   ranks its ties by id instead. Histograms use 256 LDS sub-histograms (wave, lane % 16) of
 //   16-bit counters, so lanes with equal keys rarely serialise on one counter.
@@ -181,6 +183,8 @@ constexpr int kTkHistStride = 129;  // 128 dwords of two 16-bit counters, +1 so 
 constexpr int kTkCandCap = 2048;    // candidates sorted in LDS
 constexpr int kTkResident = 19;     // 16-byte vectors per thread held in registers (rows up to 155,648 logits)
 constexpr int kTkMaxVocab = 16000000;  // keeps every 16-bit sub-histogram counter below 65,536
+constexpr int kTkRegion = 16;           // per-thread candidate entries of a register-held row
+static_assert(kTkRegion * kTkThreads * 8 <= kTkSubHists * kTkHistStride * 4, "regions fit the histograms' LDS");
 
 template <bool kVec>
 __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams p) {
@@ -188,7 +192,8 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
   __shared__ uint32_t bins[256];
   __shared__ uint32_t bin_part[4][256];
   __shared__ uint64_t cand[kTkCandCap];
-  __shared__ int32_t sel[5];  // threshold key, count above, ties needed, candidates written, ties present
+  __shared__ int32_t sel[6];  // threshold key, count above, ties needed, candidates written, ties present,
+                              // a region overflowed
   __shared__ int32_t tie_scan[kTkThreads];
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -308,17 +313,49 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
   sum_hist();
   __syncthreads();
   if (t < 64) boundary(0u, &sel[0], &sel[1], nullptr);
+  if (t == 64) sel[5] = 0;
   __syncthreads();
   const uint32_t hb = uint32_t(sel[0]);
-  // pass 2: low byte among keys in the boundary bin
-  clear_hist();
-  __syncthreads();
-  for_each([&](int, uint32_t key) {
-    if ((key >> 8) == hb) hadd(key & 255);
-  });
-  __syncthreads();
-  sum_hist();
-  __syncthreads();
+  // Rows held in registers: one sweep copies every key of the boundary bin and above, with its
+  // id, into the thread's own region of the histograms' LDS (kTkRegion entries; ids are strided
+  // over threads, so a region holds about 1/1024 of them), and the low byte and the candidates
+  // come from those entries instead of two more passes over the row. A region that overflows
+  // sends the row down the passes below.
+  uint64_t* const region = reinterpret_cast<uint64_t*>(&hist[0][0]) + t * kTkRegion;
+  bool compact = resident && sel[1] + int(bins[hb]) <= kTkRegion * kTkThreads;
+  int n_mine = 0;
+  if (compact) {
+    const uint32_t lo_key = hb << 8;
+    for_each([&](int i, uint32_t key) {
+      if (key >= lo_key) {
+        if (n_mine < kTkRegion) region[n_mine] = (uint64_t(key) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+        ++n_mine;
+      }
+    });
+    if (n_mine > kTkRegion) sel[5] = 1;
+    __syncthreads();
+    compact = sel[5] == 0;
+  }
+  if (compact) {
+    // low byte among the boundary bin's entries (a few per thread: one histogram)
+    if (t < 256) bins[t] = 0;
+    __syncthreads();
+    for (int j = 0; j < n_mine; ++j) {
+      const uint32_t key = uint32_t(region[j] >> 32);
+      if ((key >> 8) == hb) atomicAdd(&bins[key & 255], 1u);
+    }
+    __syncthreads();
+  } else {
+    // pass 2: low byte among keys in the boundary bin
+    clear_hist();
+    __syncthreads();
+    for_each([&](int, uint32_t key) {
+      if ((key >> 8) == hb) hadd(key & 255);
+    });
+    __syncthreads();
+    sum_hist();
+    __syncthreads();
+  }
   if (t < 64) {
     const uint32_t base = uint32_t(sel[1]);
     __builtin_amdgcn_wave_barrier();
@@ -340,10 +377,17 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
   };
   int n_sort;
   if (sel[1] + sel[4] <= kTkCandCap) {
-    // pass 3: every key >= the k-th; sorting puts the lowest-id ties first
-    for_each([&](int i, uint32_t key) {
-      if (key >= kth) push(i, key);
-    });
+    // every key >= the k-th (from the regions, else pass 3); sorting puts the lowest-id ties first
+    if (compact) {
+      for (int j = 0; j < n_mine; ++j) {
+        const uint64_t e = region[j];
+        if (uint32_t(e >> 32) >= kth) cand[atomicAdd(&sel[3], 1)] = e;
+      }
+    } else {
+      for_each([&](int i, uint32_t key) {
+        if (key >= kth) push(i, key);
+      });
+    }
     n_sort = sel[1] + sel[4];
   } else {
     // many equal keys at the boundary: rank the ties in id order (a contiguous chunk per
