@@ -3,8 +3,10 @@
 // * topk_candidates_kernel: the top_k logits of a row and their ids, descending, ties to the
 //   lower id. One 1024-thread workgroup per row, 16-byte loads; rows of up to 155,648 logits
 //   are read once and kept in registers as keys. Radix select on 16-bit order-preserving keys
-//   of the bf16 logits: a histogram of the high byte, then of the low byte among the boundary
-//   bin, gives the k-th key exactly (each boundary from suffix sums in one wave); every key at
+//   of the bf16 logits: the high byte of the k-th key (for register-held rows from counts at
+//   the top bins below the row's maximum, else from a histogram), then a histogram of the low
+//   byte among that bin, give the k-th key exactly (each boundary from suffix sums in one
+//   wave); every key at
 //   or above it is collected (for register-held rows from the keys of the boundary bin and
 //   above, copied once into per-thread LDS regions; else by a pass over the row) and a bitonic
 //   sort (in one wave's registers up to 64 candidates, else in LDS) orders them (ties by id),
@@ -214,7 +216,9 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
 #pragma unroll
     for (int j = 0; j < kTkResident; ++j) {
       const int v = t + j * kTkThreads;
-      const uint4 w = v < nv ? rv[v] : make_uint4(0u, 0u, 0u, 0u);
+      // slots past the row hold raw 0xffff (a negative NaN) in both halves, whose key is 0:
+      // below every threshold of the search, never its maximum
+      const uint4 w = v < nv ? rv[v] : make_uint4(~0u, ~0u, ~0u, ~0u);
       kr[j][0] = bf16x2_keys(w.x);
       kr[j][1] = bf16x2_keys(w.y);
       kr[j][2] = bf16x2_keys(w.z);
@@ -305,14 +309,75 @@ __global__ __launch_bounds__(kTkThreads) void topk_candidates_kernel(TopKParams 
     }
   };
 
-  // pass 1: high byte
-  clear_hist();
-  __syncthreads();
-  for_each([&](int, uint32_t key) { hadd(key >> 8); });
-  __syncthreads();
-  sum_hist();
-  __syncthreads();
-  if (t < 64) boundary(0u, &sel[0], &sel[1], nullptr);
+  // Pass 1: the boundary bin (high byte) of the k-th key and the keys above it. Rows held in
+  // registers first try the top of the key range: the row's largest key (packed 16-bit max)
+  // gives its high byte h, and counts of the keys at or above h, h - 1, h - 2 (packed
+  // saturating subtract, min and add: about 1.5 instructions per key, no atomics) find the
+  // boundary when it is one of those bins, as it nearly always is for logits. Otherwise, and
+  // for streamed rows, the high-byte histogram.
+  __shared__ uint32_t red[kTkThreads / 64];
+  auto block_reduce = [&](uint32_t v, bool is_max) -> uint32_t {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const uint32_t o = __shfl_xor(v, m);
+      v = is_max ? max(v, o) : v + o;
+    }
+    if (lane == 0) red[t >> 6] = v;
+    __syncthreads();
+    uint32_t acc = 0;
+#pragma unroll
+    for (int w = 0; w < kTkThreads / 64; ++w) acc = is_max ? max(acc, red[w]) : acc + red[w];
+    __syncthreads();
+    return acc;
+  };
+  bool found = false;
+  if (resident) {
+    const int nv = V >> 3;
+    // (register slots past the row hold key 0: below every threshold, never the maximum)
+    u16x2 mx2 = {0, 0};
+#pragma unroll
+    for (int j = 0; j < kTkResident; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, kr[j][e]));
+    uint32_t kmax = max(uint32_t(mx2.x), uint32_t(mx2.y));
+    for (int i = (nv << 3) + t; i < V; i += kTkThreads) kmax = max(kmax, bf16_key(row[i]));
+    kmax = block_reduce(kmax, true);
+    int b = int(kmax >> 8);
+    uint32_t above = 0;  // keys in bins above b
+    for (int it = 0; it < 3 && b >= 1; ++it, --b) {
+      const unsigned short tm1 = static_cast<unsigned short>((b << 8) - 1);
+      const u16x2 thr2 = {tm1, tm1}, one2 = {1, 1};
+      u16x2 acc2 = {0, 0};  // at most 76 keys per half
+#pragma unroll
+      for (int j = 0; j < kTkResident; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc2 += __builtin_elementwise_min(
+              __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, kr[j][e]), thr2), one2);
+      uint32_t cnt = uint32_t(acc2.x) + uint32_t(acc2.y);
+      for (int i = (nv << 3) + t; i < V; i += kTkThreads) cnt += bf16_key(row[i]) >= uint32_t(b << 8) ? 1u : 0u;
+      cnt = block_reduce(cnt, false);
+      if (cnt >= uint32_t(kk)) {
+        found = true;
+        if (t == 0) {
+          sel[0] = b;
+          sel[1] = int(above);
+          bins[b] = cnt - above;  // the only bin read before the next histogram
+        }
+        break;
+      }
+      above = cnt;
+    }
+  }
+  if (!found) {
+    clear_hist();
+    __syncthreads();
+    for_each([&](int, uint32_t key) { hadd(key >> 8); });
+    __syncthreads();
+    sum_hist();
+    __syncthreads();
+    if (t < 64) boundary(0u, &sel[0], &sel[1], nullptr);
+  }
   if (t == 64) sel[5] = 0;
   __syncthreads();
   const uint32_t hb = uint32_t(sel[0]);

@@ -36,15 +36,17 @@ def test_topk_candidates_exact(gpu, rows, vocab, k, start):
     assert torch.equal(vals.cpu().view(torch.int16), ref_v.view(torch.int16))
 
 
-@pytest.mark.parametrize("case", ["continuous", "all_equal", "misaligned", "equal_blocks", "outliers", "clustered"])
+@pytest.mark.parametrize("case", ["continuous", "all_equal", "misaligned", "equal_blocks", "outliers", "clustered",
+                                  "all_negative"])
 def test_topk_candidates_paths(gpu, case):
     """Both collection paths and both load widths: continuous logits (few ties: one pass over every
     key >= the k-th), rows of one repeated value and rows where the boundary value repeats
     thousands of times (ties overflow the candidate buffer: the id-ordered tie ranking), and a
     view whose rows start 2 bytes past a 16-byte boundary (2-byte loads); and rows whose largest
     keys are a few outliers far above the rest, so the boundary lies many bins below the
-    maximum's; and rows whose largest keys all belong to one thread (ids 8 * 1024 * j + e), so
-    its share of the candidates overflows its LDS region and the row takes the full passes."""
+    maximum's; rows whose largest keys all belong to one thread (ids 8 * 1024 * j + e), so
+    its share of the candidates overflows its LDS region and the row takes the full passes; and
+    rows of negative logits only (the register slots past a row must stay below every key)."""
     say("topk candidates path", case)
     g = torch.Generator().manual_seed(11)
     rows, vocab, k = 6, 20016, 100
@@ -55,6 +57,8 @@ def test_topk_candidates_paths(gpu, case):
         logits[1] = -3.0
     elif case == "misaligned":
         logits = (torch.randn(rows, vocab, generator=g) * 3).round().to(torch.bfloat16)
+    elif case == "all_negative":
+        logits = (-(torch.randn(rows, vocab, generator=g).abs() + 1.0)).to(torch.bfloat16)
     elif case == "clustered":
         logits = torch.randn(rows, vocab, generator=g)
         ids = torch.tensor([8192 * j + e for j in range((vocab + 8191) // 8192) for e in range(8)
