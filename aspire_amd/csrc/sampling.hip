@@ -6,11 +6,10 @@
 //   of the bf16 logits: the high byte of the k-th key (for register-held rows from counts at
 //   the top bins below the row's maximum, else from a histogram), then a histogram of the low
 //   byte among that bin, give the k-th key exactly (each boundary from suffix sums in one
-//   wave); every key at
-//   or above it is collected (for register-held rows from the keys of the boundary bin and
-//   above, copied once into per-thread LDS regions; else by a pass over the row) and a bitonic
-//   sort (in one wave's registers up to 64 candidates, else in LDS) orders them (ties by id),
-//   so the first top_k are the answer.
+//   wave); every key at or above it is collected (for register-held rows from the keys of the
+//   boundary bin and above, copied once into per-thread LDS regions; else by a pass over the
+//   row) and a bitonic sort (in one wave's registers up to 64 candidates, else in LDS) orders
+//   them (ties by id), so the first top_k are the answer.
 //   When the boundary key repeats so often that the candidates overflow LDS, an ordered pass
 //   ranks its ties by id instead. Histograms use 256 LDS sub-histograms (wave, lane % 16) of
 //   16-bit counters, so lanes with equal keys rarely serialise on one counter.
