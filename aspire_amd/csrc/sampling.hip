@@ -553,6 +553,56 @@ __global__ __launch_bounds__(kThreads) void logits_pipe_kernel(PipeParams p) {
   const int t = threadIdx.x;
   const int n = p.width;
   const int64_t r = blockIdx.x;
+  if (n <= 64) {
+    // At most 64 candidates (the top-k lists): one wave, one candidate per lane, everything in
+    // registers with the same arithmetic in the same order as below (the other waves' shares
+    // of the block reductions are the identities); no workgroup barrier.
+    if (t >= 64) return;
+    float x = -FLT_MAX, e = 0.f;
+    if (t < n) {
+      x = p.values_f32 ? static_cast<const float*>(p.values)[r * p.stride + t]
+                       : __uint_as_float(uint32_t(static_cast<const uint16_t*>(p.values)[r * p.stride + t]) << 16);
+      x *= p.inv_temperature;
+    }
+    const float wmx = fmaxf(-FLT_MAX, wave_max(x));
+    if (t < n) e = wmx == -INFINITY ? 0.f : expf(x - wmx);
+    const float wsum = wave_sum(e);
+    const float winv = wsum > 0.f ? 1.f / wsum : 0.f;
+    const float pr = e * winv;
+    float* wout = p.probs + r * p.out_stride;
+    if (!(p.top_p < 1.f)) {
+      if (t < n) wout[t] = pr;
+      return;
+    }
+    // descending bitonic sort of the probabilities' bits (non-negative floats order like
+    // integers); lanes past n hold 0
+    uint32_t v = t < n ? __float_as_uint(pr) : 0u;
+    for (int size = 2; size <= 64; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint32_t o = __shfl_xor(v, stride, 64);
+        const bool keep_max = ((t & size) == 0) == ((t & stride) == 0);
+        v = keep_max ? max(v, o) : min(v, o);
+      }
+    }
+    // prefix sums in element order; the cut is the value where the prefix first reaches top_p
+    // (the last value when none does)
+    float acc = 0.f;
+    uint32_t cut = uint32_t(__builtin_amdgcn_readlane(int(v), n - 1));
+    for (int j = 0; j < n; ++j) {
+      const float vj = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(v), j)));
+      const float prev = acc;
+      acc += vj;
+      if (acc >= p.top_p && prev < p.top_p) {
+        cut = __float_as_uint(vj);
+        break;
+      }
+    }
+    const float thresh = __uint_as_float(cut);
+    const float wkept = wave_sum(t < n && pr >= thresh ? pr : 0.f);
+    const float wrk = wkept > 0.f ? 1.f / wkept : 0.f;
+    if (t < n) wout[t] = pr >= thresh ? pr * wrk : 0.f;
+    return;
+  }
   float mx = -FLT_MAX;
   for (int i = t; i < n; i += kThreads) {
     float x = p.values_f32 ? static_cast<const float*>(p.values)[r * p.stride + i]
