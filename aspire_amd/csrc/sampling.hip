@@ -130,6 +130,28 @@ struct DrawLds {
 template <typename W>
 __device__ int block_draw(const W& w, int n, float u, DrawLds& s) {
   const int t = threadIdx.x;
+  if (n <= 64) {
+    // At most 64 weights: wave 0 alone, one weight per lane, the prefix sums added in index
+    // order (as below: one index per thread, chunk sums scanned in thread order), the first hit
+    // and the last positive index by ballots; the result reaches the other waves through LDS.
+    if (t < 64) {
+      const float x = t < n ? w(t) : 0.f;
+      float acc = 0.f, incl = 0.f;
+      for (int j = 0; j < n; ++j) {
+        acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+        incl = t == j ? acc : incl;
+      }
+      const float target = u * acc;
+      const uint64_t hits = __ballot(t < n && incl > target);
+      const uint64_t pos = __ballot(t < n && x > 0.f);
+      const int res = hits ? __builtin_ctzll(hits) : (pos ? 63 - __builtin_clzll(pos) : 0);
+      if (t == 0) s.ired[0] = res;
+    }
+    __syncthreads();
+    const int res = s.ired[0];
+    __syncthreads();  // (a later call may rewrite it)
+    return res;
+  }
   const int chunk = (n + kThreads - 1) / kThreads;
   const int i0 = min(t * chunk, n), i1 = min(i0 + chunk, n);
   float sum = 0.f;
