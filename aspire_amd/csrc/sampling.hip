@@ -782,6 +782,9 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
   __shared__ DrawLds s;
   __shared__ int local_tok[64];
   __shared__ float qx[64];
+  __shared__ float px[64];
+  __shared__ float wres[kMaxTopK + 1];
+  __shared__ float pj_l[kMaxTopK + 1];
   __shared__ int stop;
   const int64_t r = blockIdx.x;
   const int D = p.num_spec, K = p.top_k;
@@ -809,14 +812,15 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
     if (lane == 0) {
       local_tok[i] = lt;
       qx[i] = valid ? qsum : 1.f;
+      // the target probability of the local token, requested here for every position at once
+      px[i] = (lt < K && i <= n) ? tp[int64_t(i) * K + lt] : 0.f;
     }
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     int j = D;
     for (int i = 0; i < D; ++i) {
-      const int lt = local_tok[i];
-      const float pv = (lt < K && i <= n) ? tp[int64_t(i) * K + lt] : 0.f;
+      const float pv = px[i];
       if (!(u[i] * qx[i] < pv)) {
         j = i;
         break;
@@ -836,12 +840,20 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
     for (int m = 0; m < K; ++m) q += di[int64_t(j) * K + m] == id ? dp[int64_t(j) * K + m] : 0.f;
     return q;
   };
+  // P and the residual max(P - Q, 0) at position j, each computed once into LDS
   float wsum = 0.f;
-  if (j < D)
-    for (int v = threadIdx.x; v <= K; v += kThreads) wsum += fmaxf(P(v) - Q(v), 0.f);
+  for (int v = threadIdx.x; v <= K; v += kThreads) {
+    const float pv = P(v);
+    pj_l[v] = pv;
+    if (j < D) {
+      const float w = fmaxf(pv - Q(v), 0.f);
+      wres[v] = w;
+      wsum += w;
+    }
+  }
   wsum = block_sum(wsum, s.fred);
   const bool residual = j < D && wsum > 0.f;
-  const int lt = block_draw([&](int v) { return residual ? fmaxf(P(v) - Q(v), 0.f) : P(v); }, K + 1, u[D], s);
+  const int lt = block_draw([&](int v) { return residual ? wres[v] : pj_l[v]; }, K + 1, u[D], s);
   const int emitted = min(j, n);
   int64_t* out = p.output + r * (D + 1);
   for (int i = threadIdx.x; i <= D; i += kThreads) {
@@ -921,8 +933,8 @@ extern "C" int aspire_verify_topk_speculation(const float* draft_probs, const in
                                               const float* uniforms, int32_t requests, int32_t max_draft,
                                               int32_t top_k, int64_t* output, int32_t* emitted, void* stream) {
   using namespace aspire;
-  ASPIRE_CHECK_ARG(requests >= 0 && max_draft >= 1 && max_draft <= 64 && top_k >= 1,
-                   "need 1 <= max_draft <= 64 and top_k >= 1");
+  ASPIRE_CHECK_ARG(requests >= 0 && max_draft >= 1 && max_draft <= 64 && top_k >= 1 && top_k <= kMaxTopK,
+                   "need 1 <= max_draft <= 64 and 1 <= top_k <= 1024");
   if (requests == 0) return ASPIRE_OK;
   ASPIRE_CHECK_ARG(draft_probs && draft_ids && draft_tokens && draft_counts && target_probs && target_ids &&
                        uniforms && output && emitted,

@@ -516,7 +516,7 @@ int aspire_chain_speculative_sampling(const float* draft_probs, const int32_t* d
  * draft_tokens [requests, max_draft] int32, draft_counts [requests] int32, target_probs /
  * target_ids [requests, max_draft + 1, top_k], uniforms [requests, max_draft + 1];
  * output [requests, max_draft + 1] int64 (vocabulary ids, -1 past the emitted tokens),
- * emitted [requests] int32 (accepted drafts). max_draft <= 64. */
+ * emitted [requests] int32 (accepted drafts). max_draft <= 64, top_k <= 1024. */
 int aspire_verify_topk_speculation(const float* draft_probs, const int64_t* draft_ids, const int32_t* draft_tokens,
                                    const int32_t* draft_counts, const float* target_probs, const int64_t* target_ids,
                                    const float* uniforms, int32_t requests, int32_t max_draft, int32_t top_k,
