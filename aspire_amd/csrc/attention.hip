@@ -66,6 +66,7 @@ struct MergeParams {
   int64_t o_st, o_sh;
   float* lse;
   int32_t hq, group;
+  int32_t max_merge;  // merge items the plan region holds
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -926,23 +927,35 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int waves = gridDim.x * 4;
-  const int num_merge = wave_uniform(p.plan[3]);
   const MergeItem* items = reinterpret_cast<const MergeItem*>(p.plan + p.merge_off);
+  // The wave's first item is read together with the item count (one round trip instead
+  // of two); its index stays inside the plan's merge region whatever the count is.
+  const int mi_first = min(wave / kMergeTasksPerItem, p.max_merge - 1);
+  const int first_rows = wave_uniform(items[mi_first].rows);
+  const int first_row_count = wave_uniform(items[mi_first].row_count);
+  const int first_pieces = wave_uniform(items[mi_first].num_pieces);
+  const int first_row_begin = wave_uniform(items[mi_first].row_begin);
+  const int first_partial = wave_uniform(items[mi_first].first_partial_row);
+  const int first_bg = wave_uniform(items[mi_first].bg);
+  const int first_q_start = wave_uniform(items[mi_first].q_start);
+  const int num_merge = wave_uniform(p.plan[3]);
   const int gsub = lane >> 4, d8 = (lane & 15) * 8;
   for (int u = wave; u < num_merge * kMergeTasksPerItem; u += waves) {
     const int mi = u / kMergeTasksPerItem;
     const int v0 = (u - mi * kMergeTasksPerItem) * kMergeTaskUnits;
-    const int rows = wave_uniform(items[mi].rows);
-    const int row_count = wave_uniform(items[mi].row_count);
-    const int pieces = wave_uniform(items[mi].num_pieces);
+    const bool first_item = mi == mi_first;
+    const int rows = first_item ? first_rows : wave_uniform(items[mi].rows);
+    const int row_count = first_item ? first_row_count : wave_uniform(items[mi].row_count);
+    const int pieces = first_item ? first_pieces : wave_uniform(items[mi].num_pieces);
     const int s = merge_piece_groups(pieces, row_count);  // piece groups per row
     if (v0 >= row_count * s) continue;
     const int v = v0 + gsub;
     // units past the item's rows repeat its last row
-    const int row = wave_uniform(items[mi].row_begin) + min(v / s, row_count - 1);
+    const int row = (first_item ? first_row_begin : wave_uniform(items[mi].row_begin)) + min(v / s, row_count - 1);
     const int pg = v & (s - 1);
     const int my_pieces = (pieces - pg + s - 1) / s;
-    const int64_t first = wave_uniform(items[mi].first_partial_row) + int64_t(row);
+    const int64_t first =
+        (first_item ? first_partial : wave_uniform(items[mi].first_partial_row)) + int64_t(row);
     // Running (max, sum, o) over chunks of the group's pieces; within a chunk every LSE and
     // partial load is issued before any is used (one memory round trip).
     float mx = kNegInf, sum = 0.f;
@@ -1002,9 +1015,9 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
     const float inv = sum > 0.f ? 1.f / sum : 0.f;
     const int G = p.group;
     const int qi = row / G;
-    const int g = wave_uniform(items[mi].bg) & 255;
+    const int g = (first_item ? first_bg : wave_uniform(items[mi].bg)) & 255;
     const int head = g * G + (row - qi * G);
-    const int token = wave_uniform(items[mi].q_start) + qi;
+    const int token = (first_item ? first_q_start : wave_uniform(items[mi].q_start)) + qi;
     uint4 w;
     w.x = pack_bf16x2_rne(o[0] * inv, o[1] * inv);
     w.y = pack_bf16x2_rne(o[2] * inv, o[3] * inv);
@@ -1160,6 +1173,7 @@ int attention_run_impl(const aspire_plan_layout* layout, const aspire_attention_
     ASPIRE_CHECK_LAUNCH();
   }
   if (a->launch_merge) {
+    ASPIRE_CHECK_ARG(layout->max_merge > 0, "plan layout holds no merge items");
     MergeParams mp;
     mp.plan = p.plan;
     mp.merge_off = off.merge;
@@ -1171,6 +1185,7 @@ int attention_run_impl(const aspire_plan_layout* layout, const aspire_attention_
     mp.lse = p.lse;
     mp.hq = p.hq;
     mp.group = p.group;
+    mp.max_merge = layout->max_merge;
     hipLaunchKernelGGL(merge_kernel, dim3(1024), dim3(256), 0, s, mp);
     ASPIRE_CHECK_LAUNCH();
   }
