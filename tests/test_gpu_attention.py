@@ -362,3 +362,51 @@ def test_config1_full_size_sampled_rows(gpu):
                                        sub_kvl, num_kv_heads=8)
     attn_close(out[toks], ref_out)
     assert (lse[toks].cpu() - ref_lse).abs().max() < 2e-3
+
+
+def test_small_layout_merge_reads_stay_in_plan(gpu):
+    """A layout for few waves with a small int workspace holds fewer merge items (291) than
+    the merge launch has waves per item slot (4,096 waves / 12 tasks per item): every wave's
+    first-item read must stay inside the plan's merge region, and the split rows merge
+    correctly. The device buffer is exactly the layout's size."""
+    import ctypes
+
+    from aspire_amd import _lib
+
+    say("small layout merge")
+    lay = _lib.PlanLayout()
+    _lib.check(_lib.lib().aspire_plan_layout_init(8, 4, 40 << 10, 64 << 20, 128, ctypes.byref(lay)), "layout")
+    assert lay.max_merge * 12 < 4096, lay.max_merge
+    step = build_step(hq=32, hkv=8, ctx_len=[20000, 9000, 2048, 15000], q_len=[1, 4, 1, 9], is_draft=[0, 0, 1, 0],
+                      draft_budget=32, seed=21, device=gpu)
+    qo = np.ascontiguousarray(step.qo_indptr_host.numpy(), dtype=np.int32)
+    kvp = np.ascontiguousarray(step.kv_indptr_host.numpy(), dtype=np.int32)
+    kvl = np.ascontiguousarray(step.kv_len_host.numpy()[: step.batch], dtype=np.int32)
+    buf = np.zeros(lay.int_ws_bytes // 4, dtype=np.int32)
+    info = _lib.PlanInfo()
+    _lib.check(_lib.lib().aspire_plan_build(
+        ctypes.byref(lay), qo.ctypes.data_as(ctypes.c_void_p), kvp.ctypes.data_as(ctypes.c_void_p),
+        kvl.ctypes.data_as(ctypes.c_void_p), step.batch, 0, step.hq, step.hkv, PAGE, 1,
+        buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, ctypes.byref(info)), "plan")
+    assert info.num_merge > 0
+    plan_dev = torch.from_numpy(buf).to(gpu)
+    float_ws = torch.empty(lay.float_ws_bytes // 4, dtype=torch.float32, device=gpu)
+    T = step.total_tokens
+    out = torch.full_like(step.q, float("nan"))
+    k_cache, v_cache = step.cache[:, 0], step.cache[:, 1]
+    a = _lib.AttentionArgs()
+    a.q, a.q_stride_t, a.q_stride_h = step.q.data_ptr(), step.q.stride(0), step.q.stride(1)
+    a.kv_cache, a.cache_stride_p = k_cache.data_ptr(), k_cache.stride(0)
+    a.cache_stride_kv = (v_cache.data_ptr() - k_cache.data_ptr()) // 2
+    a.cache_stride_t, a.cache_stride_h = k_cache.stride(1), k_cache.stride(2)
+    a.kv_indices = step.kv_indices.data_ptr()
+    a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.lse = None
+    a.plan_dev, a.float_ws = plan_dev.data_ptr(), float_ws.data_ptr()
+    a.num_qo_heads, a.num_kv_heads, a.head_dim, a.page_size = step.hq, step.hkv, 128, PAGE
+    a.sm_scale, a.causal, a.class_mask, a.launch_merge = 1.0 / 128 ** 0.5, 1, 7, 1
+    _lib.check(_lib.lib().aspire_attention_run(ctypes.byref(lay), ctypes.byref(a), _lib.stream_of(step.q)), "run")
+    torch.cuda.synchronize()
+    ref, _ = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host,
+                             step.kv_indices.cpu(), step.kv_len_host, num_kv_heads=step.hkv)
+    attn_close(out[:T], ref[:T])
