@@ -852,11 +852,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 
 // Items of one row-tile class for this wave.
 template <int NT>
-__device__ __forceinline__ void run_class(const AttnParams& p, int c, int wave, int lane, i16x4 ident,
+__device__ __forceinline__ void run_class(const AttnParams& p, int c, int w0, int w1, int lane, i16x4 ident,
                                           bool staged, uint4* stage_lds) {
-  const int32_t* indptr = p.plan + p.indptr_off[c];
-  const int w0 = wave_uniform(indptr[wave]);
-  const int w1 = wave_uniform(indptr[wave + 1]);
   const WorkItem* items = reinterpret_cast<const WorkItem*>(p.plan + p.items_off[c]);
   for (int w = w0; w < w1; ++w) {
     WorkItem it;
@@ -905,9 +902,18 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
   __shared__ uint4 stage_lds[kLdsChunks];
   const int hpu = wave_uniform(p.plan[4]);
   const bool staged = p.staged_ok && hpu > 0 && hpu % 4 == 0;
-  if (p.class_mask & 1) run_class<1>(p, 0, wave, lane, ident, staged, stage_lds);
-  if (p.class_mask & 2) run_class<2>(p, 1, wave, lane, ident, staged, stage_lds);
-  if (p.class_mask & 4) run_class<3>(p, 2, wave, lane, ident, staged, stage_lds);
+  // every class's item range for this wave, read in one round trip at the start (a wave
+  // that finishes its class-1 items then finds empty classes 2 and 3 without waiting)
+  int w0[3], w1[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const int32_t* indptr = p.plan + p.indptr_off[c];
+    w0[c] = wave_uniform(indptr[wave]);
+    w1[c] = wave_uniform(indptr[wave + 1]);
+  }
+  if (p.class_mask & 1) run_class<1>(p, 0, w0[0], w1[0], lane, ident, staged, stage_lds);
+  if (p.class_mask & 2) run_class<2>(p, 1, w0[1], w1[1], lane, ident, staged, stage_lds);
+  if (p.class_mask & 4) run_class<3>(p, 2, w0[2], w1[2], lane, ident, staged, stage_lds);
 }
 
 // Merge of split segments. A task is (merge item, 4 units), one unit per 16-lane group: a
