@@ -53,6 +53,7 @@ EXPORTED = (
     "aspire_verify_topk_speculation",
     "aspire_prefill_block_tokens",
     "aspire_prefill_run",
+    "aspire_bandwidth_probe",
 )
 
 # Bytes of the static device scratch behind aspire_attention_run_static (ASPIRE_STATIC_SCRATCH_BYTES).
@@ -217,6 +218,7 @@ def _declare(lib):
         "aspire_verify_topk_speculation": [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
         "aspire_prefill_block_tokens": [i32, i32],
         "aspire_prefill_run": [ctypes.POINTER(PrefillArgs), vp],
+        "aspire_bandwidth_probe": [i32, vp, i64, vp, i64, i32, i32, vp],
     }
     for name, argtypes in sigs.items():
         fn = getattr(lib, name)

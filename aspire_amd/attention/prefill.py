@@ -12,6 +12,14 @@ waves (head groups that do not divide a wave's 16 query rows take the decode pat
 planner instead (rows cut into 48-query-row tiles). ``plan`` / ``run`` keep FlashInfer's
 names and argument meanings; options this path does not implement (custom masks, sliding
 windows, logit soft caps, fused RoPE) raise ``ValueError``.
+
+Graph replay: the reference builds its decode and draft wrappers of this class with
+``use_cuda_graph=True`` and replays their captured ``run`` after every re-plan
+(sparse_draft_runner.py:261-268,297-303). The prefill kernel's launch bakes in the plan's
+block count and per-plan index tensors, so with ``use_cuda_graph=True``, or whenever ``run``
+is called while the stream is capturing, the wrapper runs the decode kernel's plan instead:
+its launches read the plan from the wrapper's fixed int workspace (fixed grid, fixed
+pointers), so a graph captured after one plan replays any later one correctly.
 """
 
 from __future__ import annotations
@@ -61,7 +69,8 @@ class BatchPrefillWithPagedKVCacheWrapper(HolisticAttentionWrapper):
                      num_kv_heads, head_dim_qk, page_size, head_dim_vo=head_dim_vo, q_data_type=q_data_type,
                      causal=causal, sm_scale=sm_scale)
         self._pf = None
-        if self._kernel != "prefill" or self._has_jit:
+        if self._kernel != "prefill" or self._has_jit or self._use_cuda_graph:
+            # graph-mode wrappers keep the decode kernel's fixed-pointer plan (module docstring)
             return
         bt = int(_lib.lib().aspire_prefill_block_tokens(num_qo_heads, num_kv_heads))
         if bt <= 0:
@@ -87,7 +96,9 @@ class BatchPrefillWithPagedKVCacheWrapper(HolisticAttentionWrapper):
 
     def run(self, q: torch.Tensor, paged_kv_cache, *args, out: Optional[torch.Tensor] = None,
             lse: Optional[torch.Tensor] = None, return_lse: bool = False, **kwargs):
-        if self._pf is None:
+        if self._pf is None or torch.cuda.is_current_stream_capturing():
+            # the decode kernel's plan: also the path a capture records, since its launches
+            # read the plan from the fixed int workspace and stay valid after later plans
             res = super().run(q, paged_kv_cache, *args, out=out, return_lse=True)
             o, l_ = res
             if lse is not None:

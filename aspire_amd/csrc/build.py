@@ -22,7 +22,8 @@ PKG = HERE.parent
 LIB = PKG / "libaspire_hip.so"
 BUILD = HERE / "_build"
 SOURCES = ["capi.cpp", "plan.cpp", "host_plan.cpp", "append.hip", "page_list.hip", "attention.hip", "select.hip",
-           "rope_append.hip", "decode_ops.hip", "sampling.hip", "prefill.hip"]
+           "rope_append.hip", "decode_ops.hip", "sampling.hip", "prefill.hip",
+           "bandwidth.hip"]
 ARCH = "gfx950"
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function"]
@@ -47,8 +48,9 @@ def source_digest() -> str:
 
 
 # Per-source flags. prefill.hip: IEEE mode off, so fp32 max needs no NaN-quieting
-# canonicalisation of MFMA results (its scores are never NaN once masked).
-FILE_FLAGS = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"]}
+# canonicalisation of MFMA results (its scores are never NaN once masked). Device
+# compilation only: the host code's argument checks must still see NaN.
+FILE_FLAGS = {"prefill.hip": ["-Xarch_device", "-mno-amdgpu-ieee", "-Xarch_device", "-fno-honor-nans"]}
 
 
 def compile_one(src: str, defines: list[str], build_dir: Path = BUILD) -> Path:

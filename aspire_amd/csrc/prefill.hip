@@ -428,7 +428,10 @@ extern "C" int aspire_prefill_run(const aspire_prefill_args* a, void* stream) {
                    "cache_stride_t must be positive and below 2^26 elements (a page's rows span 32-bit offsets)");
   ASPIRE_CHECK_ARG(a->cache_stride_p > 0 && a->cache_stride_p < (int64_t(1) << 31),
                    "cache_stride_p must be positive and below 2^31 elements");
-  ASPIRE_CHECK_ARG(a->sm_scale > 0.f && a->sm_scale < 1e30f, "sm_scale must be positive and finite");
+  // by the bit pattern (positive, finite, below 1e30), which no floating-point flag can fold
+  const uint32_t scale_bits = __builtin_bit_cast(uint32_t, a->sm_scale);
+  ASPIRE_CHECK_ARG(scale_bits > 0u && scale_bits < __builtin_bit_cast(uint32_t, 1e30f),
+                   "sm_scale must be positive and finite");
   if (a->num_rows == 0 || a->total_blocks == 0) return ASPIRE_OK;
   ASPIRE_CHECK_ARG(a->q && a->kv_cache && a->kv_indices && a->kv_indptr && a->kv_last_page_len && a->qo_indptr &&
                        a->block_indptr && a->out,

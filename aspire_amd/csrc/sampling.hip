@@ -175,10 +175,14 @@ __device__ int block_draw(const W& w, int n, float u, DrawLds& s) {
   const float target = u * s.total;
   int hit = INT_MAX;
   if (i0 < i1 && s.excl[t] + s.part[t] > target) {
-    float acc = s.excl[t];
+    // The chunk's own running sum, from 0 in the order of part[t]: at the chunk's end
+    // excl + local equals excl + part (and the next chunk's excl) exactly, so a chunk whose
+    // check passes hits inside itself, and a weight of 0 never raises excl + local to a hit.
+    const float excl = s.excl[t];
+    float local = 0.f;
     for (int i = i0; i < i1; ++i) {
-      acc += w(i);
-      if (acc > target) {
+      local += w(i);
+      if (excl + local > target) {
         hit = i;
         break;
       }
@@ -687,14 +691,18 @@ __global__ __launch_bounds__(kThreads) void logits_pipe_kernel(PipeParams p) {
     cut_value = __uint_as_float(srt[n - 1]);  // no prefix reaches top_p: keep everything
   }
   __syncthreads();
-  // the smallest prefix reaching top_p ends in exactly one thread's chunk
+  // The smallest prefix reaching top_p ends in exactly one thread's chunk: the prefix at i is
+  // excl + local, local the chunk's own running sum from 0 in the order of its part, so at the
+  // chunk's end it equals the next chunk's excl exactly and the prefixes never step back.
   {
-    float acc = part[t];
-    const float before = acc;
+    const float excl = part[t];
+    float local = 0.f;
+    float prev = excl;
     for (int i = i0; i < i1; ++i) {
-      const float prev = acc;
-      acc += __uint_as_float(srt[i]);
-      if (acc >= p.top_p && (i == i0 ? before < p.top_p : prev < p.top_p)) cut_value = __uint_as_float(srt[i]);
+      local += __uint_as_float(srt[i]);
+      const float cur = excl + local;
+      if (cur >= p.top_p && prev < p.top_p) cut_value = __uint_as_float(srt[i]);
+      prev = cur;
     }
   }
   __syncthreads();
@@ -785,6 +793,8 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
   __shared__ float px[64];
   __shared__ float wres[kMaxTopK + 1];
   __shared__ float pj_l[kMaxTopK + 1];
+  __shared__ int64_t qid[kMaxTopK];  // position j's draft ids, sorted by (id, index)
+  __shared__ int32_t qidx[kMaxTopK];
   __shared__ int stop;
   const int64_t r = blockIdx.x;
   const int D = p.num_spec, K = p.top_k;
@@ -833,11 +843,52 @@ __global__ __launch_bounds__(kThreads) void verify_kernel(VerifyParams p) {
   // local distributions at position j: target P (masked past the draft count), draft Q
   const bool pj_ok = j <= n;
   auto P = [&](int v) { return (v < K && pj_ok) ? tp[int64_t(j) * K + v] : 0.f; };
+  // Q(v): the draft probability of the target's candidate v, the sum of dp[j, m] over the
+  // draft entries m with that id, in ascending m. The draft's (id, m) pairs of position j are
+  // sorted once in LDS (bitonic, padding sorts last), so each candidate finds its first pair by
+  // binary search and adds its pairs in m order: O(K log K) per request instead of a scan of
+  // all K draft ids per candidate.
+  const bool need_q = j < D && j < n;  // block-uniform
+  if (need_q) {
+    int n2 = 1;
+    while (n2 < K) n2 <<= 1;
+    for (int m = threadIdx.x; m < n2; m += kThreads) {
+      qid[m] = m < K ? di[int64_t(j) * K + m] : INT64_MAX;
+      qidx[m] = m;
+    }
+    __syncthreads();
+    for (int size = 2; size <= n2; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int a = threadIdx.x; a < n2; a += kThreads) {
+          const int b = a ^ stride;
+          if (b > a) {
+            const bool up = (a & size) == 0;
+            const int64_t ia = qid[a], ib = qid[b];
+            const int32_t ma = qidx[a], mb = qidx[b];
+            const bool a_after = ia > ib || (ia == ib && ma > mb);
+            if (a_after == up) {
+              qid[a] = ib;
+              qid[b] = ia;
+              qidx[a] = mb;
+              qidx[b] = ma;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
   auto Q = [&](int v) -> float {
-    if (v >= K || j >= n) return 0.f;  // entry K only ever lowers max(P - Q, 0), which is 0 there
+    if (v >= K || !need_q) return 0.f;  // entry K only ever lowers max(P - Q, 0), which is 0 there
     const int64_t id = ti[int64_t(j) * K + v];
+    int lo = 0, hi = K;  // first sorted pair with id >= the candidate's
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (qid[mid] < id) lo = mid + 1;
+      else hi = mid;
+    }
     float q = 0.f;
-    for (int m = 0; m < K; ++m) q += di[int64_t(j) * K + m] == id ? dp[int64_t(j) * K + m] : 0.f;
+    for (int i = lo; i < K && qid[i] == id; ++i) q += dp[int64_t(j) * K + qidx[i]];
     return q;
   };
   // P and the residual max(P - Q, 0) at position j, each computed once into LDS

@@ -522,6 +522,21 @@ int aspire_verify_topk_speculation(const float* draft_probs, const int64_t* draf
                                    const float* uniforms, int32_t requests, int32_t max_draft, int32_t top_k,
                                    int64_t* output, int32_t* emitted, void* stream);
 
+/* ----------------------------------------------------------------- (d) -- */
+/* HBM calibration (no reference counterpart: the measurement row asks for the
+ * bandwidth achieved on the box, measured with a streaming kernel, beside the
+ * published peak). mode 0 reads `bytes` of src once as 1 KiB rows, one 128-bit
+ * non-temporal buffer load per lane (the attention kernel's staged K/V access),
+ * in_flight rows per wave; dst is a sink of at least workgroups * 1024 bytes
+ * that a store reaches only under a data-dependent condition. mode 1 copies
+ * `bytes` of src to dst (dst_bytes >= bytes) with in_flight 16-byte chunks per
+ * thread. in_flight is 1, 2, 4, 8 or 16; bytes is a multiple of 1024; src and
+ * dst are 16-byte aligned; `workgroups` 256-thread workgroups stride over the
+ * buffer. Time it with events on `stream`: GB/s = bytes (x2 for the copy) /
+ * time; the best grid depends on in_flight, so sweep both. */
+int aspire_bandwidth_probe(int32_t mode, const void* src, int64_t bytes, void* dst, int64_t dst_bytes,
+                           int32_t workgroups, int32_t in_flight, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -88,6 +88,63 @@ def test_first_last_selector_against_reference_golden(gpu, name):
             assert np.array_equal(row, g("selected")[b])
 
 
+@pytest.mark.parametrize("case", ["odd_stride", "misaligned", "odd_length", "page8"])
+def test_first_last_generic_scores_kernel(gpu, case):
+    """The (R) selector's scores kernel for dumps the 16-byte vector kernel cannot read: a row
+    stride that is not a multiple of 8 entries, a dump view 2 bytes past a 16-byte boundary, a
+    max_seq_length that is not a multiple of 8, and 8-token pages. Scores equal the reference
+    chain (page_selector.py:132-138,163-181) as the oracle restates it; sets are exact wherever
+    the score gap exceeds 1e-3. Entries past a row's length are -inf, and some are NaN."""
+    say("selector generic scores", case)
+    B, H = 3, 8
+    page = 8 if case == "page8" else 16
+    max_seq = 1004 if case == "odd_length" else 1024
+    kv_stride = {"odd_stride": 1028, "odd_length": 1004}.get(case, 1024)
+    pages = (max_seq + page - 1) // page
+    gen = torch.Generator().manual_seed(12)
+    kv_len = [max_seq, 613, 37]
+    dump = (torch.randn(B, H, 2, kv_stride, generator=gen) * 6).to(torch.float16)
+    for b, n in enumerate(kv_len):
+        dump[b, :, :, n:] = float("-inf")
+    dump[0, 3, 1, ::41] = float("nan")
+    dump[1, :, 0, 200] = float("nan")  # every head NaN for one token
+    # per-page key bias so page scores separate
+    bias = (torch.randn(B, 1, 1, pages, generator=gen) * 3).repeat_interleave(page, dim=3)[..., :kv_stride]
+    dump = (dump.float() + torch.nn.functional.pad(bias, (0, kv_stride - bias.shape[-1]))).to(torch.float16)
+    qo = torch.tensor([0, 1, 5, 7], dtype=torch.int32)
+    lse = torch.randn(7, H, generator=gen) + 9
+    npg = torch.tensor([(n + page - 1) // page for n in kv_len], dtype=torch.int32)
+    table = torch.stack([torch.randperm(pages, generator=gen) + b * pages for b in range(B)]).to(torch.int32)
+    subset, L = 24, 3
+    kw = dict(pages_per_slot=pages, subset_cache_size=subset, L=L, n_heads=H, page_size=page, max_seq_length=max_seq,
+              bsz=B, head_dim=128, kv_stride=kv_stride, min_draft_pages=subset)
+    flat = dump.reshape(-1)
+    if case == "misaligned":
+        holder = torch.zeros(flat.numel() + 8, dtype=torch.float16, device=gpu)
+        dump_dev = holder[1 : 1 + flat.numel()]
+        dump_dev.copy_(flat.to(gpu))
+        assert dump_dev.data_ptr() % 16 == 2
+    else:
+        dump_dev = flat.to(gpu)
+    sel = PageSelectorFirstLastAvg(max_batch_size=B, device=gpu, dec_len=8, order="logical", **kw)
+    selected, valid = sel.select(dump_dev, lse.to(gpu), npg.to(gpu), table.to(gpu), qo.to(gpu))
+    torch.cuda.synchronize()
+    ref = FirstLastSelector(**kw)
+    ref_scores = ref.page_scores(flat, lse, qo)
+    eff = ref.effective_scores(ref_scores, npg)
+    got_scores = sel._scores[:B].cpu()
+    for b in range(B):
+        n = int(npg[b])
+        a, r = got_scores[b, :n].numpy(), ref_scores[b, :n].numpy()
+        assert np.allclose(a, r, rtol=1e-5, atol=1e-6), (b, np.abs(a - r).max())
+        k = int(valid[b])
+        assert k == min(n, subset)
+        inv = {int(p): j for j, p in enumerate(table[b].numpy())}
+        logical = [inv[int(p)] for p in selected[b, :k].cpu().numpy()]
+        assert logical == sorted(logical)
+        assert_topk_sets(logical, eff[b, :n].double().numpy(), k)
+
+
 def test_selector_logical_order_and_subset(gpu):
     z = np.load(GOLDEN)
     sel, inp, g = _golden_case(z, "small_fixed", gpu, "logical")

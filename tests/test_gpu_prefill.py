@@ -129,3 +129,69 @@ def test_prefill_head_group_outside_the_kernel_takes_the_decode_path(gpu):
     T = step.total_tokens
     attn_close(out[:T], ref_out[:T])
     assert (lse[:T].cpu() - ref_lse[:T]).abs().max() < 2e-3
+
+
+def _plan_arrays(table: torch.Tensor, q_lens, kv_lens):
+    """Reference-layout plan arrays of rows over prefixes of ``table``'s rows (host tensors)."""
+    npg = [(int(n) + PAGE - 1) // PAGE for n in kv_lens]
+    qo = torch.tensor([0, *torch.cumsum(torch.tensor(q_lens), 0).tolist()], dtype=torch.int32)
+    kvp = torch.tensor([0, *torch.cumsum(torch.tensor(npg), 0).tolist()], dtype=torch.int32)
+    idx = torch.cat([table[b, :n].cpu() for b, n in enumerate(npg)]).to(torch.int32)
+    lpl = torch.tensor([(int(n) - 1) % PAGE + 1 for n in kv_lens], dtype=torch.int32)
+    return qo, kvp, idx, lpl
+
+
+@pytest.mark.parametrize("use_cuda_graph", [True, False])
+def test_prefill_wrapper_graph_replays_later_plans(gpu, use_cuda_graph):
+    """The reference's decode/draft wrappers are this class with use_cuda_graph=True and fixed
+    index buffers, captured once and replayed after every re-plan (sparse_draft_runner.py:261-268,
+    297-303). A run captured after plan A must replay plan B (other query and key lengths, other
+    page lists, written into the same buffers) exactly as the oracle computes B; a wrapper
+    without use_cuda_graph that is captured anyway must do the same."""
+    say("prefill wrapper graph replay", use_cuda_graph)
+    step = build_step(hq=32, hkv=8, ctx_len=[2048, 1024, 704], q_len=[1, 1, 1], is_draft=[0, 0, 0],
+                      draft_budget=0, seed=36, device=gpu)
+    gen = torch.Generator(device=gpu).manual_seed(7)
+    q_buf = torch.randn(16, 32, 128, generator=gen, device=gpu).to(torch.bfloat16)
+    out_buf = torch.zeros_like(q_buf)
+    cap = int(step.block_table.numel())
+    qo_buf = torch.zeros(4, dtype=torch.int32, device=gpu)
+    kvp_buf = torch.zeros(4, dtype=torch.int32, device=gpu)
+    idx_buf = torch.zeros(cap, dtype=torch.int32, device=gpu)
+    lpl_buf = torch.zeros(3, dtype=torch.int32, device=gpu)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=gpu), "NHD", use_cuda_graph=use_cuda_graph,
+                                            qo_indptr_buf=qo_buf, paged_kv_indptr_buf=kvp_buf,
+                                            paged_kv_indices_buf=idx_buf, paged_kv_last_page_len_buf=lpl_buf)
+    cache_cpu = step.cache.cpu()
+
+    def plan(q_lens, kv_lens):
+        qo, kvp, idx, lpl = _plan_arrays(step.block_table, q_lens, kv_lens)
+        qo_buf.copy_(qo)
+        kvp_buf.copy_(kvp)
+        idx_buf[: idx.numel()].copy_(idx)
+        lpl_buf.copy_(lpl)
+        w.plan(qo_buf, kvp_buf, idx_buf, lpl_buf, 32, 8, 128, PAGE, causal=True)
+        ref_out, ref_lse = paged_attention(q_buf.cpu(), cache_cpu, qo, kvp, idx, list(kv_lens), num_kv_heads=8,
+                                           causal=True)
+        return int(qo[-1]), ref_out
+
+    plan_a = ([1, 4, 2], [300, 1000, 64])
+    plan_b = ([3, 1, 5], [2048, 90, 640])
+    T, ref = plan(*plan_a)
+    w.run(q_buf, step.cache, out=out_buf)  # eager warm-up before capture
+    torch.cuda.synchronize()
+    attn_close(out_buf[:T], ref[:T])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        w.run(q_buf, step.cache, out=out_buf)
+    for q_lens, kv_lens in (plan_a, plan_b, plan_a):
+        T, ref = plan(q_lens, kv_lens)
+        out_buf.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        attn_close(out_buf[:T], ref[:T])
+        # and the same plan eagerly (the prefill kernel when the wrapper is not in graph mode)
+        out = w.run(q_buf, step.cache)
+        torch.cuda.synchronize()
+        attn_close(out[:T], ref[:T])

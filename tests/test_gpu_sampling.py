@@ -191,10 +191,14 @@ def test_chain_keeps_the_target_distribution_on_gpu(gpu):
     assert stat < 20.52, stat                                      # chi-square 0.999 quantile, 5 dof
 
 
-def test_verify_topk_speculation_matches_oracle(gpu):
-    say("verify_topk_speculation")
-    rng = np.random.default_rng(7)
-    R, D, K, vocab = 64, 6, 50, 151936
+@pytest.mark.parametrize("R,K", [(64, 50), (16, 1024)])
+def test_verify_topk_speculation_matches_oracle(gpu, R, K):
+    """Small candidate lists and the largest top_k (1,024: the draft probabilities map onto the
+    target's candidates through the kernel's sorted id table), with a repeated draft id in one
+    row (its probabilities add up, as the reference's masked sum does)."""
+    say("verify_topk_speculation", R, K)
+    rng = np.random.default_rng(7 + K)
+    D, vocab = 6, 151936
     target_ids = np.stack([rng.choice(vocab, size=K, replace=False) for _ in range(R * (D + 1))]).reshape(R, D + 1, K)
     # draft candidates: mostly the target's, some replaced by other ids, in another order
     draft_ids = target_ids[:, :D].copy()
@@ -203,6 +207,7 @@ def test_verify_topk_speculation_matches_oracle(gpu):
             draft_ids[r, i] = rng.permutation(draft_ids[r, i])
             swap = rng.random(K) < 0.2
             draft_ids[r, i, swap] = rng.choice(vocab, size=int(swap.sum()), replace=False) + vocab
+    draft_ids[0, 0, 1] = draft_ids[0, 0, 0]
     target_probs = rng.dirichlet(np.full(K, 0.4), size=(R, D + 1)).astype(np.float32)
     draft_probs = rng.dirichlet(np.full(K, 0.4), size=(R, D)).astype(np.float32)
     tok = np.stack([[draft_ids[r, i, rng.choice(K, p=draft_probs[r, i])] for i in range(D)] for r in range(R)])
@@ -222,6 +227,76 @@ def test_verify_topk_speculation_matches_oracle(gpu):
     assert torch.equal(out.cpu()[ok], ref_out[ok])
     assert torch.equal(emitted.cpu()[ok], ref_em[ok])
     assert 0 < int(ref_em.sum()) < int(counts.sum())
+
+
+def _f32_chunk_prefixes(w: np.ndarray, threads: int = 256):
+    """The draw's fp32 chunk partition: chunk length, per-chunk sums (from 0, in index order) and
+    the exclusive prefixes of those sums in thread order, as the scan adds them."""
+    chunk = -(-w.size // threads)
+    part = np.zeros(threads, dtype=np.float32)
+    for t in range(threads):
+        acc = np.float32(0)
+        for x in w[t * chunk : (t + 1) * chunk]:
+            acc = np.float32(acc + x)
+        part[t] = acc
+    excl = np.zeros(threads + 1, dtype=np.float32)
+    for t in range(threads):
+        excl[t + 1] = np.float32(excl[t] + part[t])
+    return chunk, part, excl
+
+
+def test_draw_at_chunk_boundaries_never_takes_a_zero_weight(gpu):
+    """Inverse-CDF draws over 4,096 weights (chunks of 16 per thread) whose target sits just below
+    each chunk boundary's prefix, with the next chunk starting on a weight of 0: the drawn index
+    lies in the chunk that ends at the boundary and never has weight 0 (a draw that summed the
+    chunk in another order than its check could hit the next chunk's zero)."""
+    say("draw chunk boundaries")
+    rng = np.random.default_rng(8)
+    n = 4096
+    w = (rng.random(n) * 0.9 + 0.1).astype(np.float32) / np.float32(7.3)
+    chunk, part, excl = _f32_chunk_prefixes(w)
+    w[chunk::chunk] = 0
+    chunk, part, excl = _f32_chunk_prefixes(w)
+    total = excl[-1]
+    us, bounds = [], []
+    for c in range(1, n // chunk):
+        target = np.nextafter(excl[c], np.float32(0))             # just below the boundary prefix
+        u = np.float32(target / total)
+        while np.float32(u * total) >= excl[c]:
+            u = np.nextafter(u, np.float32(0))
+        while np.float32(np.nextafter(u, np.float32(1)) * total) < excl[c]:
+            u = np.nextafter(u, np.float32(1))
+        us.append(u)
+        bounds.append(c)
+    R = len(us)
+    probs = torch.from_numpy(np.tile(w, (R, 1))).to(gpu)
+    got = sampling_from_probs(probs, uniforms=torch.from_numpy(np.array(us, dtype=np.float32)).to(gpu)).cpu().numpy()
+    for r, c in enumerate(bounds):
+        assert w[got[r]] > 0, (c, got[r])
+        assert (c - 1) * chunk <= got[r] < c * chunk, (c, got[r])
+
+
+def test_top_p_cut_at_chunk_boundaries(gpu):
+    """Top-p over 4,096 candidates (sorted prefix sums in chunks of 16 per thread) with top_p
+    equal to the fp32 prefix at a chunk boundary: exactly one thread finds the cut, inside the
+    chunk that ends there, so the kept set is that chunk's prefix (not every candidate, and not a
+    cut past the boundary)."""
+    say("top-p chunk boundaries")
+    g = torch.Generator().manual_seed(9)
+    # distinct logits 0.002 apart: every probability differs from the next by a factor 1.002
+    vals = (torch.randperm(4096, generator=g).float() * 0.002).view(1, 4096).to(gpu)
+    pipe, _ = build_logits_pipe(0.0, 0.0)
+    probs = pipe(vals).cpu().numpy()[0]                            # the kernel's own probabilities
+    srt = np.sort(probs)[::-1].astype(np.float32)
+    assert np.unique(srt).size == srt.size
+    chunk, part, excl = _f32_chunk_prefixes(srt)
+    top_pipe, _ = build_logits_pipe(0.0, 0.5)
+    for c in (3, 17, 64, 100, 128, 181, 250):
+        top_p = float(excl[c])
+        if not 0.0 < top_p < 1.0 or not excl[c - 1] < excl[c]:
+            continue
+        kept = int((top_pipe(vals, top_p=top_p).cpu().numpy()[0] > 0).sum())
+        assert (c - 1) * chunk < kept <= c * chunk, (c, kept)
 
 
 def test_sampling_graph_replays(gpu):
