@@ -79,8 +79,12 @@ constexpr float kNegInf = -__builtin_huge_valf();
 #ifndef ASPIRE_NT1_NTLOADS
 #define ASPIRE_NT1_NTLOADS 1
 #endif
+#ifndef ASPIRE_TILE_LANES
+#define ASPIRE_TILE_LANES 2
+#endif
+// Registers: at most two waves per SIMD (256 VGPRs), or one per tile lane when there are more.
 #ifndef ASPIRE_ATTN_WAVES_PER_EU
-#define ASPIRE_ATTN_WAVES_PER_EU 2
+#define ASPIRE_ATTN_WAVES_PER_EU (ASPIRE_TILE_LANES > 2 ? ASPIRE_TILE_LANES : 2)
 #endif
 #ifndef ASPIRE_STAGED
 #define ASPIRE_STAGED 1
@@ -100,31 +104,50 @@ constexpr float kNegInf = -__builtin_huge_valf();
 #endif
 constexpr int kValuRows = 4;
 
-// Workgroup-staged K/V (1-tile items of head-aligned plans): LDS per workgroup,
-// two buffers x {K, V} x 16 key rows x 1 KiB (the rows' 4 heads), in uint4.
+// Tile lanes. A workgroup holds kAttnWavesPerBlock kv heads (the plan's waves) x kTileLanes
+// waves: the tile lanes of a head share that head's item list, and lane tl computes the
+// 16-row tiles [tl * k, min((tl + 1) * k, tiles)) of an item of `tiles` tiles, with
+// k = ceil(tiles / kTileLanes). At 3 lanes no wave carries more than one tile: a 33-48-row
+// item's three tiles run on three waves of one SIMD, whose MFMA -> softmax -> MFMA chains
+// interleave, instead of one wave's chain three tiles long. Every wave of a workgroup helps
+// stage the slot's pages; waves with no tile of an item only stage. Wave w of a workgroup
+// is tile lane w / kAttnWavesPerBlock of head lane w % kAttnWavesPerBlock.
+constexpr int kTileLanes = ASPIRE_TILE_LANES;
+static_assert(kTileLanes >= 1 && kTileLanes <= kMaxRowTiles, "1 to 3 tile lanes");
+constexpr int kWgWaves = kAttnWavesPerBlock * kTileLanes;
+
+// Workgroup-staged K/V (head-aligned plans): LDS per workgroup, two buffers x {K, V} x 16
+// key rows x 1 KiB (the rows' 4 heads), in uint4. A page's 32 row-halves (16 K rows, 16 V
+// rows) are loaded by the workgroup's waves in blocks of kStagePerWave.
 constexpr int kStageRowChunks = 64;                      // 16-byte chunks per 1 KiB row-half
 constexpr int kStageKv = 16 * kStageRowChunks;           // one of K / V
 constexpr int kStageBuf = 2 * kStageKv;                  // one buffer
 constexpr int kStageChunks = 2 * kStageBuf;              // 64 KiB
-// Per-wave V^T scratch of direct-load items (16 key rows x 16 chunks = 4 KiB per wave, when
-// ASPIRE_DIRECT_VT_MIN_NT enables it), after the stage buffers: a wave that has moved on to
-// a direct item never writes over stage buffers its workgroup's other waves may still read.
-constexpr int kVtChunks = 16 * 16;
-static_assert(kAttnWavesPerBlock == 4, "staged K/V assumes 4-wave workgroups (4 kv heads)");
-// Direct-load items with at least this many row tiles read V^T from the wave's LDS
-// scratch with transpose reads instead of transposing V rows with identity MFMAs. Off (4):
-// measured 1.7-2% slower on the long-context workload, because the V rows must be in LDS
-// before the softmax instead of before P.V, which puts the V wait on the critical path.
-#ifndef ASPIRE_DIRECT_VT_MIN_NT
-#define ASPIRE_DIRECT_VT_MIN_NT 4
+constexpr int kStageRowHalves = 32;
+// Row-tile classes of at least ASPIRE_SPLIT_MIN_TILES tiles are split over the tile lanes;
+// smaller items are computed by tile lane 0 alone (the other lanes only take the barriers).
+#ifndef ASPIRE_SPLIT_MIN_TILES
+#define ASPIRE_SPLIT_MIN_TILES 3
 #endif
-constexpr int kVtScratchChunks = ASPIRE_DIRECT_VT_MIN_NT <= kMaxRowTiles ? kAttnWavesPerBlock * kVtChunks : 0;
-// Per-wave page scores of the key-mean epilogue (64 pages, fp32), after the other areas.
+// Tile lanes whose waves load the staged pages of a split item (lane 0 alone stages the others).
+#ifndef ASPIRE_SPLIT_STAGE_LANES
+#define ASPIRE_SPLIT_STAGE_LANES 1
+#endif
+static_assert(kAttnWavesPerBlock == 4, "staged K/V assumes 4 kv heads per workgroup");
+// Per-head-lane page scores of the key-mean epilogue (64 pages, fp32), after the stage buffers.
 constexpr int kScoreChunks = kAttnWavesPerBlock * 64 / 4;
-constexpr int kLdsChunks = kStageChunks + kVtScratchChunks + kScoreChunks;
-// Issue the next page's V load right after QK^T (with K's) rather than after P.V.
-#ifndef ASPIRE_DIRECT_VT_EARLY_V
-#define ASPIRE_DIRECT_VT_EARLY_V 0
+// One 1 KiB row that the staging slots past the page's 32 row-halves write (their loads use
+// the out-of-range offset and return zeros): every wave issues the same straight-line loads
+// and stores, since loads under a per-slot branch made the compiler wait for every load in
+// flight (vmcnt(0)) before each of them.
+constexpr int kDummyChunks = kStageRowChunks;
+constexpr int kLdsChunks = kStageChunks + kScoreChunks + kDummyChunks;
+// V^T of staged items: transpose reads from LDS (ds_read_b64_tr_b16) for waves that compute
+// at least this many tiles of an item, and for every wave of a split item; the others read V
+// rows and transpose them with the identity MFMA (measured faster for 1-tile items at one
+// computing wave per SIMD).
+#ifndef ASPIRE_VT_READ_MIN_NT
+#define ASPIRE_VT_READ_MIN_NT 2
 #endif
 
 // LDS row swizzle: 16-byte chunk c of key row r is stored at chunk c ^ swz(r); swz swaps
@@ -220,9 +243,67 @@ __device__ __forceinline__ void store_dump(const AttnParams& p, int64_t idx, flo
   }
 }
 
-template <int NT, bool kValu = false>
+// The workgroup's staging of one head-aligned slot's pages (see run_item) by its first SW
+// waves: wave q < SW loads row-halves j = q * PER + i (K rows for j < 16, V rows j - 16
+// after), each one whole 1 KiB row of the slot's 4 heads, one 128-bit non-temporal load per
+// lane, and stores them to LDS chunk c ^ swz(row) of its row. kActive (q < SW) is a template
+// argument: the two roles are separate straight-line loops, since a runtime role test made
+// the compiler's wait analysis at the loop head treat the query loads as possibly pending and
+// wait for the stage loads in flight (vmcnt) before the first MFMA of every page.
+template <int SW, bool kActive>
+struct Stager {
+  static constexpr int PER = (kStageRowHalves + SW - 1) / SW;
+  const uint16_t* head0;  // the slot's first kv head in page 0 (p.cache + g0 * c_sh)
+  int64_t c_sp;
+  int span;               // bytes of a page's K and V rows of 4 heads (buffer range)
+  int offs[PER];
+  int rows_at[PER];       // LDS chunk of the lane's piece of the row-half, or -1 past the page
+  int lane;
+  uint4 st[PER];
+
+  __device__ __forceinline__ Stager(const AttnParams& p, int g0, int q, int lane_) : lane(lane_) {
+    head0 = p.cache + int64_t(g0) * p.c_sh;
+    c_sp = p.c_sp;
+    const int row_b = int(p.c_st) * 2;
+    span = int(p.c_skv) * 2 + 15 * row_b + 4 * kHeadDim * 2;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int j = q * PER + i;
+      const int kv = j >> 4, row = j & 15;
+      const bool real = j < kStageRowHalves;
+      offs[i] = real ? kv * int(p.c_skv) * 2 + row * row_b + lane * 16 : kOutOfRange;
+      rows_at[i] = real ? kv * kStageKv + row * kStageRowChunks + (lane ^ swz(row)) : -1;
+    }
+  }
+  // Every active wave issues the same straight-line loads and stores: slots past the
+  // page's 32 row-halves load zeros (out-of-range offset) and store them to the dummy LDS
+  // row. (Loads under a per-slot branch made the compiler wait for every load in flight,
+  // vmcnt(0), before each of them.)
+  __device__ __forceinline__ void load(int64_t phys, bool ok) {
+    if constexpr (!kActive) return;
+    const __amdgpu_buffer_rsrc_t rs = page_rsrc(head0 + phys * c_sp, span);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? offs[i] : kOutOfRange, 0, 2);
+      st[i] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+  }
+  __device__ __forceinline__ void store(uint4* stage_lds, int buf) const {
+    if constexpr (!kActive) return;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int at = rows_at[i] >= 0 ? buf * kStageBuf + rows_at[i] : kStageChunks + kScoreChunks + lane;
+      stage_lds[at] = st[i];
+    }
+  }
+};
+
+// One (row, kv head) piece: this wave computes NT of its tiles, from tile tile0 (rows
+// 16 * tile0 ...). compute = false: a wave with no tile of the item, which only takes its
+// part in staging the pages (staged items) or has nothing to do (direct items).
+template <int NT, int SW, bool kStage, bool kSplitItem = false, bool kValu = false>
 __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it, int lane,
-                                         i16x4 ident, bool staged, uint4* stage_lds) {
+                                         i16x4 ident, bool staged, uint4* stage_lds, int tile0, bool compute) {
   static_assert(!kValu || NT == 1, "the VALU path serves 1-tile items");
   constexpr bool kNtl = NT == 1 && ASPIRE_NT1_NTLOADS;
   const int r = lane & 15;
@@ -232,6 +313,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   const int g = it.bg & 255;
   const int rows = it.q_len * G;
   const int kv_len = it.kv_len;
+  const bool stage_path = NT <= ASPIRE_STAGED_MAX_NT && staged;
+  if (!compute && !stage_path) return;
 
   // Query fragments and per-row causal limits.
   bf16x8 qf[NT][4];
@@ -239,8 +322,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   int row_qi[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int row = t * 16 + r;
-    if (row < rows) {
+    const int row = (tile0 + t) * 16 + r;
+    if (compute && row < rows) {
       const int qi = row / G;
       const int hh = row - qi * G;
       const uint16_t* src = p.q + int64_t(it.q_start + qi) * p.q_st + int64_t(g * G + hh) * p.q_sh;
@@ -300,14 +383,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   // smallest causal limit of the item's rows (its first query token)
   const int min_limit = p.causal ? min(kv_len - it.q_len, kv_len - 1) : kv_len - 1;
   const bool do_dump = p.dump_kind != 0 && (p.dump_flags == nullptr || p.dump_flags[b] != 0);
-  // (q_len 1 rows have at most 16 query rows: one tile)
-  const bool do_score = NT == 1 && p.page_scores != nullptr && it.q_len == 1;
+  // (q_len 1 rows of at most 16 query rows: one tile, computed by tile lane 0)
+  const bool do_score = NT == 1 && compute && tile0 == 0 && p.page_scores != nullptr && it.q_len == 1 && rows <= 16;
   // key-mean epilogue: this lane's 4-key partial sums of the last 4 pages (sc0 newest) and
   // the wave's 64-page score block in LDS
   float sc0 = 0.f, sc1 = 0.f, sc2 = 0.f, sc3 = 0.f;
   float score_buf = 0.f;  // the VALU draft path's 64-page block (lane = page slot)
-  float* const score_lds = reinterpret_cast<float*>(stage_lds + kStageChunks + kVtScratchChunks) +
-                           ((threadIdx.x >> 6) & (kAttnWavesPerBlock - 1)) * 64;
+  float* const score_lds = reinterpret_cast<float*>(stage_lds + kStageChunks) +
+                           ((threadIdx.x >> 6) % kAttnWavesPerBlock) * 64;
   const int dump_slots = p.dump_kind == 2 ? 2 : 1;
   // Dump entry of each tile's row: the lane's element offset of key 0, or -1 for rows that
   // write nothing (kind 1: a row's last query; kind 2: its first and last).
@@ -319,7 +402,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     if (do_dump && qi >= 0) {
       const int slot = p.dump_kind == 2 ? (qi == 0 ? 0 : (qi == it.q_len - 1 ? 1 : -1)) : (qi == it.q_len - 1 ? 0 : -1);
       if (slot >= 0) {
-        const int head = g * G + (t * 16 + r - qi * G);
+        const int head = g * G + ((tile0 + t) * 16 + r - qi * G);
         dump_at[t] = (int64_t(b * p.dump_heads + head) * dump_slots + slot) * p.dump_stride;
       }
     }
@@ -583,39 +666,21 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 
   if constexpr (NT <= ASPIRE_STAGED_MAX_NT) {
     if (staged) {
-      // Workgroup-staged K/V. The workgroup's 4 waves hold kv heads g0..g0+3
+      // Workgroup-staged K/V. The workgroup's head lanes hold kv heads g0..g0+3
       // of one head-aligned slot: the same pages, and together 1 KiB of
-      // contiguous cache per key row (the rows' 4 heads). Wave wl loads 8 of the
-      // page's 32 row-halves (K or V, key rows 8*(wl&1)..+7) as whole 1 KiB
-      // rows, one 128-bit non-temporal load per lane and row, and stores them to
-      // LDS; after a barrier every wave reads its own head's rows from LDS in the
-      // MFMA operand layout. Contiguous 1 KiB loads stream measurably faster
-      // from HBM than 16 rows x 64 B per instruction. LDS chunk c of key row r
-      // sits at c ^ swz(r) (see swz). Two LDS buffers: page pg is read from one while
-      // page pg + 1 is stored to the other and page pg + 2 is in flight.
+      // contiguous cache per key row (the rows' 4 heads). Every wave of the
+      // workgroup loads a block of the page's 32 row-halves (K or V rows) as
+      // whole 1 KiB rows, one 128-bit non-temporal load per lane and row, and
+      // stores them to LDS; after a barrier every computing wave reads its own
+      // head's rows from LDS in the MFMA operand layout. Contiguous 1 KiB loads
+      // stream measurably faster from HBM than 16 rows x 64 B per instruction.
+      // LDS chunk c of key row r sits at c ^ swz(r) (see swz). Two LDS buffers:
+      // page pg is read from one while page pg + 1 is stored to the other and
+      // page pg + 2 is in flight. Every wave of the workgroup takes the same
+      // barriers: waves with no tile of the item stage and wait only.
       if (pb < pe) {
-        const int wl = (threadIdx.x >> 6) & 3;
-        const int kvh = wl >> 1, r0 = (wl & 1) * 8;
-        const int g0 = g & ~3, gl = g & 3;
-        const int row_b = int(p.c_st) * 2;
-        const int span = int(p.c_skv) * 2 + 15 * row_b + 4 * kHeadDim * 2;
-        const int st_off = kvh * int(p.c_skv) * 2 + r0 * row_b + lane * 16;
-        auto stage_load = [&](int64_t phys, bool ok, uint4(&st)[8]) {
-          const __amdgpu_buffer_rsrc_t rs = page_rsrc(p.cache + phys * p.c_sp + int64_t(g0) * p.c_sh, span);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? st_off + i * row_b : kOutOfRange, 0, 2);
-            st[i] = make_uint4(v.x, v.y, v.z, v.w);
-          }
-        };
-        auto stage_store = [&](int buf, const uint4(&st)[8]) {
-          uint4* base = stage_lds + buf * kStageBuf + kvh * kStageKv;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int row = r0 + i;
-            base[row * kStageRowChunks + (lane ^ swz(row))] = st[i];
-          }
-        };
+        const int gl = g & 3;
+        Stager<SW, kStage> stg(p, g & ~3, wave_uniform(threadIdx.x >> 6), lane);
         auto read_rows = [&](int buf, int kv, uint4(&dst)[4]) {
           const uint4* base = stage_lds + buf * kStageBuf + kv * kStageKv + r * kStageRowChunks;
 #pragma unroll
@@ -638,20 +703,30 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
                 (__attribute__((address_space(3))) i16x4*)(base + chunk * 16 + 8 * (j & 1)));
           }
         };
-        uint4 st[8];
-        stage_load(page_id(pb), true, st);
-        stage_store(0, st);
-        stage_load(page_id(pb + 1), pb + 1 < pe, st);
+        stg.load(page_id(pb), true);
+        stg.store(stage_lds, 0);
+        stg.load(page_id(pb + 1), pb + 1 < pe);
         stage_barrier();
         int64_t id_ahead = page_id(pb + 2);
         int pg = pb;
+        if (!compute) {
+          do {
+            stg.store(stage_lds, ((pg - pb) & 1) ^ 1);
+            const int64_t nphys = id_ahead;
+            id_ahead = page_id(pg + 3);
+            stg.load(nphys, pg + 2 < pe);
+            stage_barrier();
+          } while (++pg < pe);
+          return;
+        }
         do {
           const int buf = (pg - pb) & 1;
           uint4 kr[4];
-          // V^T by transpose reads for 2-tile items; 1-tile items read V rows
-          // (conflict-free 128-bit reads) and transpose them with the identity
-          // MFMA, which measured faster there
-          using VSrc = std::conditional_t<(NT >= 2), i16x4[8], uint4[4]>;
+          // V^T by transpose reads for waves of ASPIRE_VT_READ_MIN_NT tiles or more; the
+          // others read V rows (conflict-free 128-bit reads) and transpose them with the
+          // identity MFMA, which measured faster for 1-tile items at one wave per SIMD
+          constexpr bool kVtRead = NT >= ASPIRE_VT_READ_MIN_NT || kSplitItem;
+          using VSrc = std::conditional_t<kVtRead, i16x4[8], uint4[4]>;
           VSrc vs;
           read_rows(buf, 0, kr);
           page_body(
@@ -660,7 +735,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
                 // keys past kv_len (only on a segment's last page) may hold stale
                 // values: zero them so 0 * stale cannot reach the sums
                 const bool tail = pg * 16 + 16 > kv_len;
-                if constexpr (NT >= 2) {
+                if constexpr (kVtRead) {
                   read_vt(buf, vs);
                   if (tail) {
                     const int k0 = pg * 16 + 4 * grp;
@@ -681,10 +756,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
                 }
               },
               [&] {
-                stage_store(buf ^ 1, st);
+                stg.store(stage_lds, buf ^ 1);
                 const int64_t nphys = id_ahead;
                 id_ahead = page_id(pg + 3);
-                stage_load(nphys, pg + 2 < pe, st);
+                stg.load(nphys, pg + 2 < pe);
                 stage_barrier();
               });
         } while (++pg < pe);
@@ -692,12 +767,15 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     }
   }
 
+  if (!compute) return;  // (a staged piece with no pages)
+
   // One K/V register buffer pipelined at half-page granularity: the next
   // page's K is requested as soon as this page's QK^T has consumed K, and its V
   // as soon as P.V has consumed each V slice (about one page in flight per
   // wave, 32 VGPRs; a second buffer measured no faster). Prologue and loop
   // share one block so the loop head sees a single, straight-line load order.
-  if (!(NT <= ASPIRE_STAGED_MAX_NT && staged) && pb < pe) {
+  // (Tile lanes of one direct item each load the pages they compute on.)
+  if (!stage_path && pb < pe) {
     uint4 kr[4], vr[4];
     {
       const int64_t phys = page_id(pb);
@@ -708,55 +786,15 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     }
     int64_t id_ahead = page_id(pb + 1);
     int pg = pb;
-    if constexpr (!kValu && NT >= ASPIRE_DIRECT_VT_MIN_NT) {
-      // V^T through the wave's LDS scratch: the page's V rows (keys past kv_len arrive as
-      // zeros) are written in the swizzled row layout and read back transposed, the PV
-      // MFMA's A operand. Both next-page loads are issued once QK^T has consumed K and the
-      // V rows are in LDS, so two loads are in flight during the softmax. LDS operations
-      // of one wave complete in order, so the read after the write and the next page's
-      // write after this page's reads need no wait.
-      uint4* vt_lds = stage_lds + kStageChunks + ((threadIdx.x >> 6) & (kAttnWavesPerBlock - 1)) * kVtChunks;
-      const int vt_row = 4 * grp + (r >> 2);
-      do {
-        const bool has_next = pg + 1 < pe;
-        const int64_t next_phys = id_ahead;
-        id_ahead = page_id(pg + 2);
-        const bool next_ok = has_next && (pg + 1) * 16 + r < kv_len;
-        i16x4 vt[8];
-        page_body(
-            pg, kr, vt,
-            [&] {
-#pragma unroll
-              for (int c = 0; c < 4; ++c) vt_lds[r * 16 + ((4 * c + grp) ^ swz(r))] = vr[c];
-              const char* base = reinterpret_cast<const char*>(vt_lds + vt_row * 16);
-#pragma unroll
-              for (int j = 0; j < 8; ++j) {
-                const int chunk = (4 * (j >> 1) + (r & 3)) ^ swz(vt_row);
-                vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) i16x4*)(base + chunk * 16 + 8 * (j & 1)));
-              }
-              load_k(next_phys, next_ok, kr);
-#if ASPIRE_DIRECT_VT_EARLY_V
-              load_v(next_phys, next_ok, vr);
-#endif
-            },
-            [&] {
-#if !ASPIRE_DIRECT_VT_EARLY_V
-              load_v(next_phys, next_ok, vr);
-#endif
-            });
-      } while (++pg < pe);
-    } else {
-      do {
-        const bool has_next = pg + 1 < pe;
-        const int64_t next_phys = id_ahead;
-        id_ahead = page_id(pg + 2);
-        // Issued unconditionally (straight-line code keeps the wait counts
-        // exact); past the item's last page the out-of-range offset returns zeros.
-        const bool next_ok = has_next && (pg + 1) * 16 + r < kv_len;
-        page_body(pg, kr, vr, [&] { load_k(next_phys, next_ok, kr); }, [&] { load_v(next_phys, next_ok, vr); });
-      } while (++pg < pe);
-    }
+    do {
+      const bool has_next = pg + 1 < pe;
+      const int64_t next_phys = id_ahead;
+      id_ahead = page_id(pg + 2);
+      // Issued unconditionally (straight-line code keeps the wait counts
+      // exact); past the item's last page the out-of-range offset returns zeros.
+      const bool next_ok = has_next && (pg + 1) * 16 + r < kv_len;
+      page_body(pg, kr, vr, [&] { load_k(next_phys, next_ok, kr); }, [&] { load_v(next_phys, next_ok, vr); });
+    } while (++pg < pe);
   }
 
   if constexpr (kValu) {
@@ -815,7 +853,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
     float lt = l[t];
     lt += shfl_xor_f(lt, 16);
     lt += shfl_xor_f(lt, 32);
-    const int row = t * 16 + r;
+    const int row = (tile0 + t) * 16 + r;
     if (row >= rows) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     const float lse_v = lt > 0.f ? m[t] + __builtin_log2f(lt) : kNegInf;
@@ -850,10 +888,39 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
   }
 }
 
-// Items of one row-tile class for this wave.
-template <int NT>
+// One item of a class for this wave: n of its tiles from tile0 (n = K or the short share R;
+// 0: no tile), kStage: the wave loads a block of the staged pages.
+template <int TILES, int K, int R, int SW, bool kStage, bool kSplit>
+__device__ __forceinline__ void run_class_item(const AttnParams& p, const WorkItem& it, int lane, i16x4 ident,
+                                               bool stg, uint4* stage_lds, int tile0, int n) {
+  if constexpr (TILES == 1 && ASPIRE_DRAFT_VALU) {
+    if (it.q_len * p.group <= kValuRows) {
+      run_item<1, SW, kStage, false, true>(p, it, lane, ident, stg, stage_lds, tile0, n > 0);
+      return;
+    }
+  }
+  if (n == K) {
+    run_item<K, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, true);
+  } else if constexpr (R > 0) {
+    if (n == R) run_item<R, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, true);
+    else run_item<K, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, false);
+  } else {
+    run_item<K, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, false);
+  }
+}
+
+// Items of one row-tile class (TILES 16-row tiles) for this wave, tile lane tl of its head.
+template <int TILES>
 __device__ __forceinline__ void run_class(const AttnParams& p, int c, int w0, int w1, int lane, i16x4 ident,
-                                          bool staged, uint4* stage_lds) {
+                                          bool staged, uint4* stage_lds, int tl) {
+  constexpr bool kSplit = TILES >= ASPIRE_SPLIT_MIN_TILES;
+  constexpr int LANES = kSplit ? kTileLanes : 1;             // lanes that compute this class
+  constexpr int K = (TILES + LANES - 1) / LANES;             // tiles per computing lane
+  constexpr int R = TILES % K;                               // the last computing lane's share, if short
+  constexpr int SW = kAttnWavesPerBlock * (kSplit ? ASPIRE_SPLIT_STAGE_LANES : 1);  // staging waves
+  const int tile0 = tl * K;
+  const int n = tl < LANES ? min(K, TILES - tile0) : 0;
+  const bool stager = wave_uniform(threadIdx.x >> 6) < SW;
   const WorkItem* items = reinterpret_cast<const WorkItem*>(p.plan + p.items_off[c]);
   for (int w = w0; w < w1; ++w) {
     WorkItem it;
@@ -866,28 +933,30 @@ __device__ __forceinline__ void run_class(const AttnParams& p, int c, int w0, in
     it.page_end = wave_uniform(items[w].page_end);
     it.bg = wave_uniform(items[w].bg);
     it.partial_row = wave_uniform(items[w].partial_row);
-    // the flag is a property of the row, so the workgroup's 4 waves (heads of one
-    // slot, walking the same rows) all take the same path
-    const bool stg = staged && !(q_len_flags & kItemDirect);
-    if constexpr (NT == 1 && ASPIRE_DRAFT_VALU) {
-      if (it.q_len * p.group <= kValuRows) {
-        run_item<1, true>(p, it, lane, ident, stg, stage_lds);
-        continue;
-      }
+    // The flag is a property of the row, so the workgroup's waves (heads of one slot and
+    // their tile lanes, walking the same rows) all take the same path, and so take the same
+    // barriers; the class's tiles per lane (K) decide it for every lane alike.
+    const bool stg = staged && !(q_len_flags & kItemDirect) && K <= ASPIRE_STAGED_MAX_NT;
+    constexpr bool kSplitItems = kSplit && LANES > 1;
+    if (stager) {
+      run_class_item<TILES, K, R, SW, true, kSplitItems>(p, it, lane, ident, stg, stage_lds, tile0, n);
+    } else {
+      run_class_item<TILES, K, R, SW, false, kSplitItems>(p, it, lane, ident, stg, stage_lds, tile0, n);
     }
-    run_item<NT>(p, it, lane, ident, stg, stage_lds);
   }
 }
 
 // One persistent launch for all row-tile classes: each wave runs its class-1
 // items, then class 2, then class 3 (the planner balances every class over
-// the waves), so the launch has one ramp and one tail. Registers follow the
-// 3-tile class (at most 2 waves per SIMD); the default grid runs one wave per
-// SIMD.
-__global__ __launch_bounds__(64 * kAttnWavesPerBlock)
+// the head waves), so the launch has one ramp and one tail. A workgroup is
+// kAttnWavesPerBlock head waves of the plan x kTileLanes tile lanes; the
+// default grid runs one head wave per SIMD (plus its tile lanes).
+__global__ __launch_bounds__(64 * kWgWaves)
 __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_kernel(AttnParams p) {
   const int lane = threadIdx.x & 63;
-  const int wave = wave_uniform(blockIdx.x * kAttnWavesPerBlock + (threadIdx.x >> 6));
+  const int wl = wave_uniform(threadIdx.x >> 6);
+  const int tl = wl / kAttnWavesPerBlock;
+  const int wave = wave_uniform(blockIdx.x * kAttnWavesPerBlock + wl % kAttnWavesPerBlock);
   if (wave >= p.num_waves) return;
   // Identity B operand: lane holds B[k = 4*grp + j][n = r] = (k == n).
   const int r = lane & 15, grp = lane >> 4;
@@ -896,7 +965,7 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
   uint32_t e1 = (4 * grp + 2 == r ? one : 0u) | ((4 * grp + 3 == r ? one : 0u) << 16);
   const i16x4 ident = as_i16x4(e0, e1);
   // Head-aligned plans (header[4] = kv heads per slot, a multiple of 4) give
-  // the 4 waves of a workgroup the same pages: their 1-tile items stage K/V
+  // the head lanes of a workgroup the same pages: their items stage K/V
   // through LDS. The flag is uniform over the workgroup, so every wave takes
   // the same barriers.
   __shared__ uint4 stage_lds[kLdsChunks];
@@ -911,9 +980,9 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
     w0[c] = wave_uniform(indptr[wave]);
     w1[c] = wave_uniform(indptr[wave + 1]);
   }
-  if (p.class_mask & 1) run_class<1>(p, 0, w0[0], w1[0], lane, ident, staged, stage_lds);
-  if (p.class_mask & 2) run_class<2>(p, 1, w0[1], w1[1], lane, ident, staged, stage_lds);
-  if (p.class_mask & 4) run_class<3>(p, 2, w0[2], w1[2], lane, ident, staged, stage_lds);
+  if (p.class_mask & 1) run_class<1>(p, 0, w0[0], w1[0], lane, ident, staged, stage_lds, tl);
+  if (p.class_mask & 2) run_class<2>(p, 1, w0[1], w1[1], lane, ident, staged, stage_lds, tl);
+  if (p.class_mask & 4) run_class<3>(p, 2, w0[2], w1[2], lane, ident, staged, stage_lds, tl);
 }
 
 // Merge of split segments. A task is (merge item, 4 units), one unit per 16-lane group: a
@@ -1169,13 +1238,14 @@ int attention_run_impl(const aspire_plan_layout* layout, const aspire_attention_
                 (a->cache_stride_kv + 15 * a->cache_stride_t + 4 * kHeadDim) * 2 < (int64_t(1) << 30);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((layout->num_waves + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock);
+  const dim3 block(64 * kWgWaves);
   for (int c = 0; c < 3; ++c) {
     p.indptr_off[c] = off.indptr[c];
     p.items_off[c] = off.items[c];
   }
   p.class_mask = a->class_mask & 7;
   if (p.class_mask) {
-    hipLaunchKernelGGL(attention_kernel, grid, dim3(64 * kAttnWavesPerBlock), 0, s, p);
+    hipLaunchKernelGGL(attention_kernel, grid, block, 0, s, p);
     ASPIRE_CHECK_LAUNCH();
   }
   if (a->launch_merge) {

@@ -59,6 +59,12 @@ CASES = [
     ("gqa2_qwen17b", 16, 8, [4096, 4096, 1000, 77], [1, 5, 7, 16], [1, 0, 0, 0]),
     ("mha_gqa1", 8, 8, [129, 250], [3, 16], [0, 0]),
     ("gqa8", 64, 8, [300, 999], [2, 6], [0, 0]),
+    # 3-tile items whose tiles run on two waves of a head: GQA 2 (tile 2 holds tokens 16..23),
+    # 4 kv heads (a slot of one workgroup), and 2 kv heads (not head-aligned: every lane of a
+    # split item loads its own pages)
+    ("gqa2_tile3_split", 16, 8, [2000, 333, 4097], [24, 17, 20], [0, 0, 0]),
+    ("gqa4_hkv4_tile3", 16, 4, [3000, 1000, 40], [9, 12, 11], [0, 0, 0]),
+    ("gqa8_hkv2_direct_tile3", 16, 2, [1500, 700], [5, 6], [0, 0]),
 ]
 
 
