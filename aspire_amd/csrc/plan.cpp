@@ -28,18 +28,15 @@ namespace aspire {
 namespace {
 
 constexpr int kMinPagesPerWave = 8;
-// Stream-K cost units of one page-head: a 1- or 2-tile item staged for the workgroup's heads
-// (8), a 1- or 2-tile item reading its own head's list (direct: 12) and a 3-tile item (9),
-// chosen by sweeping them on mixed workloads (configs 3 and 4 at every draft fraction).
+// Stream-K cost units of one page-head: an item staged for the workgroup's heads (8, every
+// row-tile class: 3-tile items run their tiles on two waves of the head and stream at the
+// staged rate; sweeping 7-10 for them on config 4 gave 8), and an item reading its own head's
+// list (direct: 12, from a sweep of 10-13 on configs 3 and 4).
 #ifndef ASPIRE_DIRECT_PAGE_COST
 #define ASPIRE_DIRECT_PAGE_COST 12
 #endif
-#ifndef ASPIRE_THREE_TILE_PAGE_COST
-#define ASPIRE_THREE_TILE_PAGE_COST 9
-#endif
 constexpr int64_t kDirectPageCost = ASPIRE_DIRECT_PAGE_COST;
 constexpr int64_t kSharedPageCost = 8;
-constexpr int64_t kThreeTilePageCost = ASPIRE_THREE_TILE_PAGE_COST;
 
 struct Segment {
   int32_t q_start, q_len, kv_len, list_base, npages, bg, rows;
@@ -212,10 +209,7 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
   // (class by class, segments in row order), so a slot streams one contiguous range of that
   // sequence and a long row is split about as often as its share of the whole launch needs,
   // not once per slot of its class.
-  auto page_cost = [&](int c, bool direct) -> int64_t {
-    if (c == 2) return kThreeTilePageCost;
-    return direct ? kDirectPageCost : kSharedPageCost;
-  };
+  auto page_cost = [&](int, bool direct) -> int64_t { return direct ? kDirectPageCost : kSharedPageCost; };
   int64_t T = 0, T_pages = 0;
   for (int c = 0; c < 3; ++c)
     for (const auto& s : sc.segs[c]) {
