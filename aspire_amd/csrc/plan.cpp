@@ -28,15 +28,23 @@ namespace aspire {
 namespace {
 
 constexpr int kMinPagesPerWave = 8;
-// Stream-K cost units of one page-head: an item staged for the workgroup's heads (8, every
-// row-tile class: 3-tile items run their tiles on two waves of the head and stream at the
-// staged rate; sweeping 7-10 for them on config 4 gave 8), and an item reading its own head's
-// list (direct: 12, from a sweep of 10-13 on configs 3 and 4).
+// Stream-K cost units of one page-head, in quarters: an item staged for the workgroup's heads
+// (32 for 2- and 3-tile items, 33 for 1-tile items) and an item reading its own head's list
+// (direct: 48). Per-wave finish times of config-4 launches (fitted per class) showed 1-tile
+// pages about 3-10% slower than 3-tile pages in a joint launch, whose tiles run on two waves
+// of the head; sweeping the 1-tile weight (32-35) gave 33 at every draft fraction, and the
+// 3-tile weight (28-40) 32. The direct weight comes from a sweep of 40-52 on configs 3 and 4.
 #ifndef ASPIRE_DIRECT_PAGE_COST
-#define ASPIRE_DIRECT_PAGE_COST 12
+#define ASPIRE_DIRECT_PAGE_COST 48
+#endif
+#ifndef ASPIRE_C1_PAGE_COST
+#define ASPIRE_C1_PAGE_COST 33
+#endif
+#ifndef ASPIRE_C2_PAGE_COST
+#define ASPIRE_C2_PAGE_COST 32
 #endif
 constexpr int64_t kDirectPageCost = ASPIRE_DIRECT_PAGE_COST;
-constexpr int64_t kSharedPageCost = 8;
+constexpr int64_t kSharedPageCost[3] = {ASPIRE_C1_PAGE_COST, ASPIRE_C2_PAGE_COST, 32};
 
 struct Segment {
   int32_t q_start, q_len, kv_len, list_base, npages, bg, rows;
@@ -209,7 +217,7 @@ int plan_core(const aspire_plan_layout* layout, const int32_t* qo_indptr, const 
   // (class by class, segments in row order), so a slot streams one contiguous range of that
   // sequence and a long row is split about as often as its share of the whole launch needs,
   // not once per slot of its class.
-  auto page_cost = [&](int, bool direct) -> int64_t { return direct ? kDirectPageCost : kSharedPageCost; };
+  auto page_cost = [&](int c, bool direct) -> int64_t { return direct ? kDirectPageCost : kSharedPageCost[c]; };
   int64_t T = 0, T_pages = 0;
   for (int c = 0; c < 3; ++c)
     for (const auto& s : sc.segs[c]) {
