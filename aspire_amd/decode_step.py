@@ -17,12 +17,24 @@ and the residual adds, norms, SwiGLU step and token pick are the row kernels of
 the HIP library (``aspire_add_rms_norm``, ``aspire_silu_mul``,
 ``aspire_argmax_rows``), so a whole step can be recorded in one HIP graph.
 
-Refresh layer: at ``refresh_layer`` every row attends its full context and the
-kernel writes the key-mean page scores of the single-query (draft) rows; the
-top-``budget`` pages per (row, KV head), the last ``recent_pages`` forced in,
-become the draft rows' per-head page lists (verify rows keep one shared list,
-their full table, and the kernel's staged row path) for the layers after it, and for the layers before it in the next step. Before
-the first step every draft segment lists its row's last ``budget`` pages.
+Refresh layer, ``selector="keymean"`` (BASELINE config 2's selection): at
+``refresh_layer`` every row attends its full context and the kernel writes the
+key-mean page scores of the single-query (draft) rows; the top-``budget`` pages
+per (row, KV head), the last ``recent_pages`` forced in, become the draft rows'
+per-head page lists (verify rows keep one shared list, their full table, and the
+kernel's staged row path) for the layers after it, and for the layers before it
+in the next step. Before the first step every draft segment lists its row's last
+``budget`` pages.
+
+Refresh layer, ``selector="first_last"`` (the reference's own selection): the
+refresh layer's full attention also writes the fp16 first/last logits dump of
+every row and its LSE (the dump op of base.py:452-514); at the start of the next
+step, as the reference's step preparation does (base.py:580-667,708-716),
+``PageSelectorFirstLastAvg`` selects each row's top-``budget`` pages from them
+(the last ``recent_pages`` forced in, default 8 as config.py:29), and
+``build_unified_indices`` makes one page list per row (the draft rows' selection,
+the verify rows' table; base.py:1200-1256) that every layer of the step except
+the refresh layer attends, on the kernel's staged row path.
 """
 
 from __future__ import annotations
@@ -35,10 +47,10 @@ import torch
 import torch.nn.functional as F
 
 from aspire_amd import _lib
-from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
+from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper, build_holistic_dump_jit_args
 from aspire_amd.attention.page_list import build_head_page_lists, build_unified_indices
 from aspire_amd.attention.rope import RopeConfig, qk_norm_rope_update_kv
-from aspire_amd.backends.page_selector import KeyMeanPageSelector
+from aspire_amd.backends.page_selector import KeyMeanPageSelector, PageSelectorFirstLastAvg
 
 PAGE = 16
 DRAFT_MODE, VERIFY_MODE = 0, 1
@@ -205,8 +217,14 @@ class MixedDecodeStep:
     """
 
     def __init__(self, weights: DecodeWeights, caches: torch.Tensor, ctx_len, q_len, is_draft,
-                 block_table: torch.Tensor, *, budget: int = 128, refresh_layer: int = 2, recent_pages: int = 1,
-                 tokens: torch.Tensor | None = None, seed: int = 0, waves_per_cu: int | None = None):
+                 block_table: torch.Tensor, *, budget: int = 128, refresh_layer: int = 2,
+                 recent_pages: int | None = None, selector: str = "keymean", tokens: torch.Tensor | None = None,
+                 seed: int = 0, waves_per_cu: int | None = None):
+        if selector not in ("keymean", "first_last"):
+            raise ValueError("selector must be 'keymean' or 'first_last'")
+        self.selector_kind = selector
+        if recent_pages is None:
+            recent_pages = 8 if selector == "first_last" else 1
         shape = weights.shape
         self.shape, self.w, self.caches = shape, weights, caches
         dev = caches.device
@@ -302,7 +320,34 @@ class MixedDecodeStep:
         self.selector.page_scores.zero_()  # verify rows' segments are ranked too (their lists are unused)
 
         ws = torch.empty(1, device=dev)
-        self.refresh_wrapper = HolisticAttentionWrapper(ws, "NHD", waves_per_cu=waves_per_cu)
+        dump_args = None
+        if selector == "first_last":
+            # the first/last dump of the refresh layer and the reference selector over it
+            W = table.shape[1]
+            self.kv_stride = W * PAGE  # a multiple of the kernel's KV tile (compute_max_cta_tile_kv)
+            self.dump = torch.full((B * shape.n_head * 2 * self.kv_stride,), float("-inf"), dtype=torch.float16,
+                                   device=dev)
+            self.lse_buf = torch.zeros(self.T, shape.n_head, dtype=torch.float32, device=dev)
+            self.fl_selector = PageSelectorFirstLastAvg(
+                max_batch_size=B, pages_per_slot=W, subset_cache_size=self.budget, L=self.recent_pages,
+                n_heads=shape.n_head, page_size=PAGE, max_seq_length=W * PAGE, device=dev, bsz=B,
+                dec_len=int(ql.max()), head_dim=shape.head_dim, kv_stride=self.kv_stride, order="logical")
+            rcnt = np.where(dr, np.minimum(self.budget, self.num_pages_host), self.num_pages_host)
+            rptr = np.zeros(B + 1, dtype=np.int64)
+            rptr[1:] = np.cumsum(rcnt)
+            self.row_indptr = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+            self.row_indices = torch.zeros(max(int(rptr[-1]), 1), dtype=torch.int32, device=dev)
+            self.row_indptr_host = torch.from_numpy(rptr.astype(np.int32))
+            self.row_kv_len_host = torch.from_numpy(((rcnt - 1) * PAGE + self.last_host).astype(np.int32))
+            self.row_counts_host = rcnt
+            # before the first selection: every draft row lists its last `budget` pages
+            self.fl_selector._selected_buf[:B].copy_(self.selector.selected[:, 0])
+            self.fl_selector._valid_counts_buf[:B].copy_(self.selector.counts[:, 0])
+            self.fl_selected = self.fl_selector._selected_buf[:B, : self.budget]
+            self.fl_valid = self.fl_selector._valid_counts_buf[:B]
+            dump_args = build_holistic_dump_jit_args(torch.bfloat16, shape.head_dim, dump_kind="first_last_compact",
+                                                     dump_buffer_dtype=torch.float16)
+        self.refresh_wrapper = HolisticAttentionWrapper(ws, "NHD", jit_args=dump_args, waves_per_cu=waves_per_cu)
         self.mixed_wrapper = HolisticAttentionWrapper(ws, "NHD", waves_per_cu=waves_per_cu)
         self.rope = RopeConfig(rope_theta=shape.rope_base)
 
@@ -334,14 +379,33 @@ class MixedDecodeStep:
         s = self.shape
         self.refresh_wrapper.plan_host(self.qo_host, self.full_indptr_host, self.full_kv_len_host, self.full_indices,
                                        s.n_head, s.n_local_heads, 128, PAGE, causal=True)
-        self.mixed_wrapper.plan_segments(self.qo_host, self.seg_start_host, self.seg_pages_host,
-                                         self.mixed_kv_len_host, self.mixed_indices, s.n_head, s.n_local_heads, 128,
-                                         PAGE, causal=True)
+        if self.selector_kind == "first_last":
+            # a draft row keeps min(budget, pages) pages (draft_percent=None), so the plan
+            # needs no device readback of the selector's counts
+            self.mixed_wrapper.plan_host(self.qo_host, self.row_indptr_host, self.row_kv_len_host, self.row_indices,
+                                         s.n_head, s.n_local_heads, 128, PAGE, causal=True)
+        else:
+            self.mixed_wrapper.plan_segments(self.qo_host, self.seg_start_host, self.seg_pages_host,
+                                             self.mixed_kv_len_host, self.mixed_indices, s.n_head, s.n_local_heads,
+                                             128, PAGE, causal=True)
 
     def build_lists(self) -> None:
-        """Device page lists: the full row lists and the per-head lists from the current selection."""
+        """Device page lists: the full row lists and the draft lists from the current selection."""
         self._full_lists()
-        self._head_lists()
+        if self.selector_kind == "first_last":
+            self._row_lists()
+        else:
+            self._head_lists()
+
+    def _row_lists(self) -> None:
+        build_unified_indices(self.mode_flags, self.fl_selected, self.block_table, self.fl_valid, self.num_pages,
+                              self.row_indices, self.row_indptr)
+
+    def select_first_last(self) -> None:
+        """The reference's step-preparation replan (base.py:580-667,1200-1256): select every
+        row's pages from the last refresh layer's dump and LSE, then rebuild the row lists."""
+        self.fl_selector.select(self.dump, self.lse_buf, self.num_pages, self.block_table, self.qo_indptr)
+        self._row_lists()
 
     def _full_lists(self) -> None:
         build_unified_indices(self.all_verify, self.block_table, self.block_table, self.num_pages, self.num_pages,
@@ -355,7 +419,11 @@ class MixedDecodeStep:
 
     def attention(self, layer: int, q: torch.Tensor) -> None:
         cache = self.caches[layer]
-        if layer == self.refresh_layer:
+        if layer == self.refresh_layer and self.selector_kind == "first_last":
+            _, lse = self.refresh_wrapper.run(q, cache, self.dump, self.shape.n_head, self.kv_stride, out=self.y,
+                                              return_lse=True)
+            self.lse_buf.copy_(lse[: self.T])
+        elif layer == self.refresh_layer:
             self.refresh_wrapper.run(q, cache, out=self.y, page_scores=self.selector.page_scores)
             self.selector.select(self.num_pages, self.block_table, self.batch)
             self._head_lists()
@@ -373,6 +441,8 @@ class MixedDecodeStep:
         T = self.T
         qs, kvs = s.q_size, s.kv_size
         self._full_lists()
+        if self.selector_kind == "first_last":
+            self.select_first_last()
         torch.index_select(w.tok_embeddings, 0, self.tokens, out=self.x)
         ffn_out = None
         for layer, lw in enumerate(w.layers):
@@ -407,6 +477,8 @@ class MixedDecodeStep:
         every layer's attention, the refresh selection; q is whatever ``qkv`` holds."""
         s = self.shape
         self._full_lists()
+        if self.selector_kind == "first_last":
+            self.select_first_last()
         q = self.qkv[:, : s.q_size].view(self.T, s.n_head, s.head_dim)
         for layer in range(s.n_layer):
             self.attention(layer, q)
@@ -417,11 +489,21 @@ class MixedDecodeStep:
         segments read one head's K and V per page), appends, logits."""
         s = self.shape
         refresh_kv = int(self.ctx_len.sum()) * s.n_local_heads * s.head_dim * 2 * 2
-        mixed_kv = int(self.mixed_kv_len_host.numpy().astype(np.int64).sum()) * s.head_dim * 2 * 2
+        if self.selector_kind == "first_last":
+            mixed_kv = int(self.row_kv_len_host.numpy().astype(np.int64).sum()) * s.n_local_heads * s.head_dim * 2 * 2
+        else:
+            mixed_kv = int(self.mixed_kv_len_host.numpy().astype(np.int64).sum()) * s.head_dim * 2 * 2
         kv = refresh_kv + (s.n_layer - 1) * mixed_kv
         weights = s.n_layer * self.w.layer_bytes() + self.w.output.numel() * 2 + s.dim * 2
         embed = self.T * s.dim * 2
         append = s.n_layer * self.T * s.kv_size * 2 * 2
         logits = self.T * s.vocab_size * 2
-        total = kv + weights + embed + append + logits
-        return {"kv": kv, "weights": weights, "append": append, "logits": logits, "total": total}
+        out = {"kv": kv, "weights": weights, "append": append, "logits": logits}
+        if self.selector_kind == "first_last":
+            # fp16 dump entries the refresh layer writes (first and last query of each row, one
+            # entry when they coincide) and the selector's read of both slots of every page
+            slots = np.where(self.q_len > 1, 2, 1)
+            out["dump_write"] = int((slots * self.ctx_len).sum()) * s.n_head * 2
+            out["dump_read"] = int(self.num_pages_host.sum()) * PAGE * s.n_head * 2 * 2
+        out["total"] = sum(out.values())
+        return out

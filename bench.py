@@ -71,6 +71,9 @@ def parse():
                          "step); 2: refresh layer; 3: the full 36-layer decode step alone; 4: the long-context "
                          "layer at --draft-frac")
     ap.add_argument("--draft-frac", type=float, default=0.5, help="config 4: fraction of drafting rows")
+    ap.add_argument("--selector", choices=["keymean", "first_last"], default="keymean",
+                    help="config 3: the refresh layer's page selection (key-mean per KV head, or the reference's "
+                         "first/last dump selector per row)")
     ap.add_argument("--class-mask", type=int, default=0,
                     help="config 4: plan only the rows of these row-tile classes (bit c-1 for class c: <=16, <=32, "
                          "<=48 query rows) and time their attention launch, no merge; value counts their KV bytes "
@@ -219,7 +222,7 @@ def main():
     torch.cuda.set_device(dev)
     log(_lib.build_info())
     if args.config == 3:
-        dec = measure_config3(args.decode_steps, min(args.warmup, 20), args.waves_per_cu)
+        dec = measure_config3(args.decode_steps, min(args.warmup, 20), args.waves_per_cu, selector=args.selector)
         line = {
             "metric": "decode tokens/s (Qwen3-8B shape, 36 layers, B=64, ctx U[8k,32k], 50/50 draft/verify)",
             "value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.decode_steps,
@@ -327,6 +330,8 @@ def main():
     decode = None
     if args.config == 1 and not args.no_decode:
         decode = measure_config3(args.decode_steps, min(args.warmup, 20), args.waves_per_cu)
+        decode["first_last"] = measure_config3(args.decode_steps, min(args.warmup, 20), args.waves_per_cu,
+                                               selector="first_last")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -749,10 +754,13 @@ def measure_config4(steps, waves_per_cu, fracs=(0.0, 0.25, 0.5, 0.75, 1.0)):
     return res
 
 
-def measure_config3(steps, warmup, waves_per_cu):
+def measure_config3(steps, warmup, waves_per_cu, selector="keymean"):
     """Config 3: one full 36-layer Qwen3-8B decode step (batch 64, contexts U[8k, 32k], 32 draft rows
-    over top-128 per-KV-head page lists refreshed at layer 2, 32 verify rows with q_len U{2..9}),
-    recorded in one HIP graph and replayed. Returns tokens/s, step time and the attention share."""
+    over top-128 page lists refreshed at layer 2, 32 verify rows with q_len U{2..9}), recorded in
+    one HIP graph and replayed. ``selector``: "keymean" (per-KV-head key-mean lists) or
+    "first_last" (the reference's first/last dump, per-row selection and row lists). Returns
+    tokens/s, step time and the attention share."""
+    from aspire_amd.attention.holistic_wrapper import HolisticAttentionWrapper
     from aspire_amd.decode_step import QWEN3_8B, DecodeWeights, MixedDecodeStep, alloc_kv_caches
     from aspire_amd.workloads import PAGE, config3_rows, random_block_table
 
@@ -766,9 +774,9 @@ def measure_config3(steps, warmup, waves_per_cu):
     weights = DecodeWeights(shape, dev, seed=0)
     caches = alloc_kv_caches(shape, pool, dev, seed=0)
     step = MixedDecodeStep(weights, caches, ctx, ql, dr, torch.from_numpy(table), budget=128, refresh_layer=2,
-                           waves_per_cu=waves_per_cu)
+                           selector=selector, waves_per_cu=waves_per_cu)
     torch.cuda.synchronize()
-    log(f"config3: built in {time.time() - t0:.1f}s: {int(dr.sum())} draft + {int((~dr).sum())} verify rows, "
+    log(f"config3 ({selector}): built in {time.time() - t0:.1f}s: {int(dr.sum())} draft + {int((~dr).sum())} verify rows, "
         f"{step.T} tokens, pool {pool} pages x {shape.n_layer} layers "
         f"({caches.numel() * 2 / 1e9:.1f} GB KV), weights {(shape.n_layer * weights.layer_bytes() + 2 * weights.output.numel() * 2) / 1e9:.1f} GB")
     reps = 10
@@ -802,18 +810,39 @@ def measure_config3(steps, warmup, waves_per_cu):
     for _ in range(3):
         attn_graph.replay()
     attn_ms = timed(attn_graph.replay, steps, stream)
+    extra = {}
+    if selector == "first_last":
+        # the refresh layer with its dump against the same attention without it, and the
+        # selection + row lists of the step's preparation, each graph-timed on its own
+        q = step.qkv[:, : shape.q_size].view(step.T, shape.n_head, shape.head_dim)
+        cache = step.caches[step.refresh_layer]
+        plain = HolisticAttentionWrapper(torch.empty(1, device=dev), "NHD", waves_per_cu=waves_per_cu)
+        plain.plan(step.qo_indptr, step.full_indptr, step.full_indices, step.last_page_len, shape.n_head,
+                   shape.n_local_heads, 128, PAGE, causal=True)
+        with_dump = lambda: step.attention(step.refresh_layer, q)
+        no_dump = lambda: plain.run(q, cache, out=step.y)
+        extra = {"refresh_layer_us": round(graph_timed(with_dump, steps, stream) * 1e3, 1),
+                 "refresh_layer_us_without_dump": round(graph_timed(no_dump, steps, stream) * 1e3, 1),
+                 "selection_and_lists_us": round(graph_timed(step.select_first_last, steps, stream) * 1e3, 1)}
+        extra["dump_cost_share_of_refresh_layer"] = round(
+            1 - extra["refresh_layer_us_without_dump"] / extra["refresh_layer_us"], 4)
+        del plain
     nb = step.algorithmic_bytes()
     tps = step.T / (ms * 1e-3)
     gbs = nb["total"] / (ms * 1e-3) / 1e9
     attn_gbs = nb["kv"] / (attn_ms * 1e-3) / 1e9
-    log(f"config3: step {ms:.2f} ms (eager {eager_ms:.2f} ms) -> {tps:.0f} tokens/s, {gbs:.0f} GB/s; "
-        f"attention {attn_ms:.2f} ms ({attn_ms / ms:.1%}) at {attn_gbs:.0f} GB/s; "
+    log(f"config3 ({selector}): step {ms:.2f} ms (eager {eager_ms:.2f} ms) -> {tps:.0f} tokens/s, {gbs:.0f} GB/s; "
+        f"attention {attn_ms:.2f} ms ({attn_ms / ms:.1%}) at {attn_gbs:.0f} GB/s; {extra} "
         f"measured in {time.perf_counter() - t1:.1f}s")
+    sel_text = ("top-128 pages per KV head by key-mean score, refreshed at layer 2" if selector == "keymean" else
+                "top-128 pages per row by the reference's first/last selector (PageSelectorFirstLastAvg, last 8 "
+                "pages forced) over the fp16 first/last logits dump of layer 2, selected in the next step's "
+                "preparation; one page list per row (build_unified_indices)")
     res = {
         "workload": ("config3: full 36-layer Qwen3-8B decode step (hidden 4096, 32/8 heads, SwiGLU 12288, "
-                     "qk-norm, RoPE 1e6), batch 64, contexts U[8192, 32768], 32 draft rows (q_len 1, top-128 "
-                     "pages per KV head by key-mean score, refreshed at layer 2) + 32 verify rows (q_len "
-                     "U{2..9}); one HIP graph per step, greedy token pick"),
+                     f"qk-norm, RoPE 1e6), batch 64, contexts U[8192, 32768], 32 draft rows (q_len 1, {sel_text}) "
+                     "+ 32 verify rows (q_len U{2..9}); one HIP graph per step, greedy token pick"),
+        "selector": selector,
         "tokens_per_s": round(tps, 1),
         "step_ms": round(ms, 3),
         "eager_step_ms": round(eager_ms, 3),
@@ -827,6 +856,7 @@ def measure_config3(steps, warmup, waves_per_cu):
         "plan_host_us": round(plan_us, 1),
         "verify_q_len": ql[~dr].tolist(),
         "timing": {"prewarm_ms": round(pw_ms, 1), "per_step": summary(per_step)},
+        **extra,
     }
     del graph, attn_graph, step, caches, weights
     torch.cuda.empty_cache()

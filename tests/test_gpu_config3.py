@@ -160,3 +160,132 @@ def _check(step, shape, ctx, ql, dr, table, gpu):
         assert torch.equal(glogits, logits), f"replay {rep} logits"
         _ = torch.randn(1000, device=gpu).sum().item()   # eager work between replays
     del graph
+
+
+def test_config3_first_last_refresh(gpu):
+    """The reference's own refresh inside the config-3 step (selector="first_last"): the refresh
+    layer writes the fp16 first/last logits dump and the LSE of every row; the next step's
+    preparation selects each row's top-128 pages with PageSelectorFirstLastAvg (last 8 forced in)
+    and builds one list per row with build_unified_indices, which the mixed layers attend. Checks:
+    * page scores equal the oracle's restatement of page_selector.py on the GPU's own dump and
+      LSE, and the selected sets are exact wherever the score gap exceeds 1e-3 (all 64 rows);
+    * the refresh layer's dump of sampled rows equals fp16(q.k) of the oracle (one fp16 step);
+    * in the refresh layer and two mixed layers, 2 draft rows (over their selection) and 2 verify
+      rows (one with q_len 9, over the full table) equal the oracle;
+    * the step recorded in one HIP graph (selection included) replays to the eager ids and logits.
+    """
+    from oracle.attention import DumpSpec
+    from oracle.select import FirstLastSelector
+    from helpers import assert_topk_sets
+
+    say("config3 (R): 36-layer Qwen3-8B step, B=64, first/last refresh")
+    torch.cuda.empty_cache()
+    shape = QWEN3_8B
+    ctx, ql, dr = config3_rows(seed=0)
+    n_pages = (ctx + PAGE - 1) // PAGE
+    table, pool = random_block_table(n_pages, seed=0)
+    weights = DecodeWeights(shape, gpu, seed=0)
+    caches = alloc_kv_caches(shape, pool, gpu, seed=0)
+    step = MixedDecodeStep(weights, caches, ctx, ql, dr, torch.from_numpy(table), budget=128, refresh_layer=2,
+                           selector="first_last")
+    try:
+        B, T, Hq = step.batch, step.T, shape.n_head
+        W, stride = table.shape[1], step.kv_stride
+        say("config3 (R): step 1")
+        step.forward()
+        torch.cuda.synchronize()
+        dump, lse = step.dump.cpu(), step.lse_buf.cpu()
+        qo = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+        say("config3 (R): selection")
+        step.select_first_last()
+        torch.cuda.synchronize()
+        sel = step.fl_selected.cpu().numpy()
+        valid = step.fl_valid.cpu().numpy()
+        got_scores = step.fl_selector._scores[:B].cpu().numpy()
+        ref = FirstLastSelector(pages_per_slot=W, subset_cache_size=128, L=8, n_heads=Hq, page_size=PAGE,
+                                max_seq_length=W * PAGE, bsz=B, kv_stride=stride)
+        ref_scores = ref.page_scores(dump, lse, torch.from_numpy(qo))
+        eff = ref.effective_scores(ref_scores, torch.from_numpy(n_pages.astype(np.int32))).double().numpy()
+        ref_scores = ref_scores.numpy()
+        for b in range(B):
+            n = int(n_pages[b])
+            assert np.allclose(got_scores[b, :n], ref_scores[b, :n], rtol=1e-5, atol=1e-6), b
+            k = int(valid[b])
+            assert k == min(128, n)
+            inv = {int(p): j for j, p in enumerate(table[b, :n])}
+            logical = [inv[int(p)] for p in sel[b, :k]]
+            assert logical == sorted(logical) and logical[-1] == n - 1, b
+            assert_topk_sets(logical, eff[b, :n], k)
+        del ref_scores, eff
+
+        say("config3 (R): step 2 with the selection")
+        state = [step.dump, step.lse_buf]
+        saved = [t.clone() for t in state]
+        cap = {}
+        ids = step.forward(capture=cap).clone()
+        logits = step.logits.clone()
+        torch.cuda.synchronize()
+        assert torch.isfinite(logits.float()).all()
+        row_ptr = step.row_indptr.cpu().numpy()
+        row_idx = step.row_indices.cpu().numpy()
+        drafts, verify = np.flatnonzero(dr), np.flatnonzero(~dr)
+        v9 = int(verify[np.flatnonzero(ql[verify] == 9)[0]])
+        rows = [int(drafts[0]), int(drafts[-1]), v9, int(verify[np.argmin(ql[verify])])]
+        dump2 = step.dump.view(B, Hq, 2, stride)
+        for layer in (2, 20, 35):
+            say(f"config3 (R): layer {layer}")
+            y = cap[f"y{layer}"]
+            for b in rows:
+                toks = range(int(qo[b]), int(qo[b + 1]))
+                if layer == step.refresh_layer or not dr[b]:
+                    pages, lens = table[b, : n_pages[b]], [int(ctx[b])]
+                else:
+                    pages = row_idx[row_ptr[b] : row_ptr[b + 1]]
+                    assert pages.tolist() == sel[b, : valid[b]].tolist()
+                    lens = [int(valid[b] - 1) * PAGE + (int(ctx[b]) - 1) % PAGE + 1]
+                kw = {}
+                if layer == step.refresh_layer:
+                    ref_dump = torch.full((Hq * 2 * stride,), float("-inf"), dtype=torch.float16)
+                    kw["dump"] = DumpSpec(buffer=ref_dump, kind="first_last", num_heads=Hq, kv_stride=stride)
+                ref_out, _ = oracle_row(cap[f"q{layer}"], step.caches[layer], toks, pages, lens, shape.n_local_heads,
+                                        **kw)
+                attn_close(y[list(toks)], ref_out)
+                if layer == step.refresh_layer:
+                    got = dump2[b].cpu().float().reshape(-1)
+                    want = ref_dump.float()
+                    written = torch.isfinite(want)
+                    slots = 2 if ql[b] > 1 else 1
+                    # the row's written entries (slot 1 of a single-query row keeps its earlier values)
+                    mask = written.view(Hq, 2, stride)[:, :slots].reshape(-1)
+                    g2 = got.view(Hq, 2, stride)[:, :slots].reshape(-1)
+                    w2 = want.view(Hq, 2, stride)[:, :slots].reshape(-1)
+                    assert torch.equal(torch.isfinite(g2), mask), b
+                    assert torch.allclose(g2[mask], w2[mask], rtol=2e-3, atol=2e-3), b
+        del cap
+
+        say("config3 (R): graph replay")
+        for t, s_ in zip(state, saved):
+            t.copy_(s_)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step.forward()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gids = step.forward()
+        glogits = step.logits
+        for rep in range(2):
+            for t, s_ in zip(state, saved):
+                t.copy_(s_)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(gids, ids), f"replay {rep} ids"
+            assert torch.equal(glogits, logits), f"replay {rep} logits"
+            _ = torch.randn(1000, device=gpu).sum().item()
+        del graph
+    finally:
+        del step, caches, weights
+        torch.cuda.empty_cache()
