@@ -149,6 +149,68 @@ class PageSelectorFirstLastAvg(PageSelector):
 
     _slots = 2
 
+    def _run_compact(self, logits, first_lse, last_lse, num_pages, block_table):
+        """Scores + top-k over ``logits [R, H, 2, S]`` with per-row LSEs ``[R, H]``: the LSE rows
+        are stacked as (first, last) pairs and addressed through qo_indptr = [0, 2, ..., 2R],
+        so the kernels read exactly the rows select() reads through the token indptr."""
+        R, H = logits.shape[0], logits.shape[1]
+        if logits.dim() != 4 or logits.shape[2] != 2 or H != self.n_heads:
+            raise ValueError("logits must be [rows, n_heads, 2, seq_len]")
+        if first_lse.shape != (R, H) or last_lse.shape != (R, H):
+            raise ValueError("first_lse and last_lse must be [rows, n_heads]")
+        if logits.dtype != torch.float16:
+            raise ValueError("the HIP selector reads an fp16 logits dump")
+        stride = logits.stride(2)
+        if logits.stride(3) != 1 or logits.stride(1) != 2 * stride or logits.stride(0) != H * 2 * stride:
+            logits = logits.contiguous()
+            stride = logits.shape[3]
+        seq_len = logits.shape[3]
+        if seq_len > self.pages_per_slot * self.page_size:
+            raise ValueError("seq_len exceeds pages_per_slot * page_size")
+        if num_pages.dtype != torch.int32 or block_table.dtype != torch.int32 or block_table.stride(1) != 1:
+            raise ValueError("num_pages and block_table must be int32 with contiguous rows")
+        if num_pages.numel() < R or block_table.shape[0] < R:
+            raise ValueError("num_pages and block_table must cover every row")
+        _lib.require_cuda(logits, first_lse, last_lse, num_pages, block_table,
+                          what="PageSelectorFirstLastAvg.select_from_compact_first_last")
+        lse = torch.stack([first_lse, last_lse], dim=1).to(torch.float32).reshape(2 * R, H).contiguous()
+        qo = torch.arange(0, 2 * R + 1, 2, dtype=torch.int32, device=logits.device)
+        npg = num_pages.contiguous()
+        scores, selected, valid = self._buffers(R)
+        stream = _lib.stream_of(logits)
+        L = _lib.lib()
+        rc = L.aspire_select_first_last_scores(
+            _lib.ptr(logits), stride, self.n_heads, R, seq_len, _lib.ptr(lse), 2 * R, _lib.ptr(qo), _lib.ptr(npg),
+            None, R, self.page_size, float(self._sm_scale_log2e), _lib.ptr(scores), scores.stride(0), 2, stream)
+        _lib.check(rc, "PageSelectorFirstLastAvg.select_from_compact_first_last")
+        mode, subset, min_pages, pct = self._count_mode()
+        rc = L.aspire_select_topk(
+            _lib.ptr(scores), scores.stride(0), _lib.ptr(npg), None, R, 1, int(self.L), mode, int(subset),
+            int(min_pages), float(pct), _lib.ptr(block_table), block_table.stride(0), _ORDERS[self._order],
+            _lib.ptr(selected), selected.stride(0), self.subset_cache_size, _lib.ptr(valid), stream)
+        _lib.check(rc, "PageSelectorFirstLastAvg.select_from_compact_first_last")
+        return selected[:, : self.subset_cache_size], valid
+
+    def select_from_compact_first_last(self, logits, first_lse, last_lse, num_pages, block_table):
+        """``logits [B, H, 2, seq_len]`` (a view of the dump is fine), ``first_lse`` / ``last_lse``
+        ``[B, H]``: the same selection as ``select`` with the LSEs given per row
+        (page_selector.py:183-184)."""
+        return self._run_compact(logits, first_lse, last_lse, num_pages, block_table)
+
+    def select_layers_from_compact_first_last(self, logits, first_lse, last_lse, num_pages, block_table):
+        """``logits [n_layers, B, H, 2, kv_stride]``, LSEs ``[n_layers, B, H]``: every layer's rows
+        selected in one pass (page counts and tables repeated per layer); returns
+        ``(selected [n_layers, B, k], valid_counts [B])`` (page_selector.py:186-204)."""
+        n_layers, batch = logits.shape[:2]
+        flat = logits.reshape(n_layers * batch, self.n_heads, 2, logits.shape[-1])
+        if flat.shape[-1] != self.max_seq_length:
+            flat = flat[..., : self.max_seq_length]
+        selected, valid = self._run_compact(
+            flat, first_lse.reshape(n_layers * batch, self.n_heads), last_lse.reshape(n_layers * batch, self.n_heads),
+            num_pages[:batch].to(torch.int32).repeat(n_layers).contiguous(),
+            block_table[:batch].repeat(n_layers, 1).contiguous())
+        return selected.view(n_layers, batch, self.subset_cache_size), valid[:batch]
+
 
 class KeyMeanPageSelector:
     """Top-k pages per (request, KV head) by the key-mean score.

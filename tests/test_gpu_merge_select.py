@@ -145,6 +145,72 @@ def test_first_last_generic_scores_kernel(gpu, case):
         assert_topk_sets(logical, eff[b, :n].double().numpy(), k)
 
 
+@pytest.mark.parametrize("name", ["small_fixed", "percent", "ties_inf"])
+def test_compact_first_last_against_reference_golden(gpu, name):
+    """select_from_compact_first_last (page_selector.py:183-184): the dump as a [B, H, 2, seq_len]
+    view and the first / last query rows' LSEs given per row select exactly what select() does
+    through the token indptr, and match the reference-recorded selections."""
+    say("compact selector golden", name)
+    z = np.load(GOLDEN)
+    sel, inp, g = _golden_case(z, name, gpu, "physical")
+    B, H, page, max_seq, kv_stride = (int(x) for x in g("params")[:5])
+    qo = g("qo_indptr").astype(np.int64)
+    lse = inp["lse_buffer"]
+    top = lse.shape[0] - 1
+    first = lse[torch.from_numpy(np.clip(qo[:B], 0, top)).to(gpu)]
+    last = lse[torch.from_numpy(np.clip(qo[1 : B + 1] - 1, 0, top)).to(gpu)]
+    logits = inp["attention_weights_buffer"][: B * H * 2 * kv_stride].view(B, H, 2, kv_stride)[..., :max_seq]
+    got, got_valid = (t.clone() for t in sel.select_from_compact_first_last(
+        logits, first, last, inp["num_pages"], inp["block_table"]))
+    want, want_valid = sel.select(**inp)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(got_valid, want_valid)
+    assert np.array_equal(got_valid.cpu().numpy(), g("valid"))
+    if name != "ties_inf":
+        assert np.array_equal(got.cpu().numpy(), g("selected"))
+
+
+def test_compact_first_last_layers(gpu):
+    """select_layers_from_compact_first_last (page_selector.py:186-204): three layers' dumps in one
+    call equal three single-layer calls, and each layer's sets match the oracle wherever the score
+    gap exceeds 1e-3; the counts are the first layer's (every layer has the same pages)."""
+    say("compact selector, layers")
+    n_layers, B, H, page, max_seq = 3, 4, 8, 16, 1024
+    kv_stride = 1040
+    gen = torch.Generator().manual_seed(17)
+    logits = (torch.randn(n_layers, B, H, 2, kv_stride, generator=gen) * 5).to(torch.float16)
+    npg = torch.tensor([64, 40, 3, 17], dtype=torch.int32)
+    for b, n in enumerate(npg.tolist()):
+        logits[:, b, :, :, n * page :] = float("-inf")
+    first = torch.randn(n_layers, B, H, generator=gen) + 8
+    last = torch.randn(n_layers, B, H, generator=gen) + 8
+    table = torch.stack([torch.randperm(64, generator=gen) + 64 * b for b in range(B)]).to(torch.int32)
+    kw = dict(max_batch_size=n_layers * B, pages_per_slot=64, subset_cache_size=12, L=2, n_heads=H, page_size=page,
+              max_seq_length=max_seq, device=gpu, bsz=B, dec_len=4, kv_stride=kv_stride)
+    sel = PageSelectorFirstLastAvg(**kw)
+    d = lambda t: t.to(gpu)
+    got, valid = (t.clone() for t in sel.select_layers_from_compact_first_last(d(logits), d(first), d(last), d(npg),
+                                                                                 d(table)))
+    assert got.shape == (n_layers, B, 12) and valid.shape == (B,)
+    ref = FirstLastSelector(pages_per_slot=64, subset_cache_size=12, L=2, n_heads=H, page_size=page,
+                            max_seq_length=max_seq, bsz=B, kv_stride=kv_stride)
+    for layer in range(n_layers):
+        one, one_valid = sel.select_from_compact_first_last(d(logits[layer, ..., :max_seq]), d(first[layer]),
+                                                            d(last[layer]), d(npg), d(table))
+        torch.cuda.synchronize()
+        assert torch.equal(got[layer], one) and torch.equal(valid, one_valid), layer
+        # the oracle's select() through a token indptr whose first / last rows carry these LSEs
+        lse = torch.stack([first[layer], last[layer]], dim=1).reshape(2 * B, H)
+        qo = torch.arange(0, 2 * B + 1, 2, dtype=torch.int32)
+        scores = ref.page_scores(logits[layer].reshape(-1), lse, qo)
+        eff = ref.effective_scores(scores, npg)
+        for b in range(B):
+            n, k = int(npg[b]), int(valid[b])
+            assert k == min(n, 12)
+            inv = {int(x): j for j, x in enumerate(table[b].tolist())}
+            assert_topk_sets([inv[int(x)] for x in got[layer, b, :k].cpu().tolist()], eff[b, :n].double().numpy(), k)
+
+
 def test_selector_logical_order_and_subset(gpu):
     z = np.load(GOLDEN)
     sel, inp, g = _golden_case(z, "small_fixed", gpu, "logical")
