@@ -85,6 +85,9 @@ def parse():
                     help="skip the per-component measurements (append, page list, merge, selectors, refresh layer)")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 full decode step")
     ap.add_argument("--decode-steps", type=int, default=30, help="timed graph replays of the config-3 step")
+    ap.add_argument("--no-calibration", action="store_true",
+                    help="skip the on-box HBM calibration (roofline.measured_peak_gbs is then null); for "
+                         "counter passes")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (read + write) for rocprofv3 counter calibration")
     ap.add_argument("--prewarm-ms", type=float, default=1000.0,
@@ -310,9 +313,12 @@ def main():
         f"{attn_ms * 1e3:.1f} us (median {np.median(attn_per) * 1e3:.1f}) -> {achieved:.0f} GB/s "
         f"({achieved / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
-    calib = measure_hbm_calibration(dev, stream)
-    log(f"HBM calibration: streaming read {calib['measured_peak_gbs']:.0f} GB/s (best grid), copy "
-        f"{calib['copy_gbs']:.0f} GB/s; attention kernel at {achieved / calib['measured_peak_gbs']:.1%} of the read")
+    calib = None
+    if not args.no_calibration:
+        calib = measure_hbm_calibration(dev, stream)
+        log(f"HBM calibration: streaming read {calib['measured_peak_gbs']:.0f} GB/s (best grid), copy "
+            f"{calib['copy_gbs']:.0f} GB/s; attention kernel at {achieved / calib['measured_peak_gbs']:.1%} of the "
+            "read")
 
     if args.calibrate_copy:
         src = torch.empty(1 << 29, dtype=torch.int16, device=dev).random_()
@@ -393,8 +399,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": measured_traffic(args.config),
-            "measured_peak_gbs": calib["measured_peak_gbs"],
-            "frac_of_measured": round(achieved / calib["measured_peak_gbs"], 4),
+            "measured_peak_gbs": calib["measured_peak_gbs"] if calib else None,
+            "frac_of_measured": round(achieved / calib["measured_peak_gbs"], 4) if calib else None,
             "calibration": calib,
             "kernel_us": round(attn_ms * 1e3, 2),
             "bytes_per_launch": attn_bytes,
