@@ -7,7 +7,7 @@ cached prefix plus the new tokens, page lists as for decode. ``run`` launches th
 dedicated prefill kernel (``aspire_prefill_run``): each workgroup takes one query block
 (``aspire_prefill_block_tokens(hq, hkv)`` tokens of one row, all G query heads of one kv
 head) and stages every page of its keys once in LDS, two pages per step, for all of its
-waves (head groups that do not divide a wave's 16 query rows take the decode path below).
+waves (head groups that do not divide a wave's 32 query rows take the decode path below).
 ``kernel="decode"`` runs the mixed decode kernel and its
 planner instead (rows cut into 48-query-row tiles). ``plan`` / ``run`` keep FlashInfer's
 names and argument meanings; options this path does not implement (custom masks, sliding
@@ -74,7 +74,7 @@ class BatchPrefillWithPagedKVCacheWrapper(HolisticAttentionWrapper):
             return
         bt = int(_lib.lib().aspire_prefill_block_tokens(num_qo_heads, num_kv_heads))
         if bt <= 0:
-            # a head group that does not divide a wave's 16 query rows (e.g. 6 or 12 query heads
+            # a head group that does not divide a wave's 32 query rows (e.g. 6 or 12 query heads
             # per kv head): the mixed kernel's query tiles serve the plan made above
             return
         # rows: the entries of kv_last_page_len (FlashInfer's batch), with their query blocks
