@@ -244,36 +244,45 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   };
 
   const int vt_row = 4 * grp + (r >> 2);
-  auto compute = [&](const uint4* kb, int s) {
-    const int key0 = s * kPfStepKeys;
-    // S^T of both pages: lane (r, grp) holds keys key0 + 4grp + i (sa) and key0 + 16 + 4grp + i (sb)
-    f32x4 sa[kPfTiles], sb[kPfTiles];
-    {
-      uint4 kr[4];
+  // S^T of the wave's current step: lane (r, grp) holds keys key0 + 4grp + i (sa) and
+  // key0 + 16 + 4grp + i (sb); P of the step in bf16 for P.V
+  f32x4 sa[kPfTiles], sb[kPfTiles];
+  bf16x8 pf[kPfTiles];
+  // this lane's K chunks (column reads) and V^T transpose reads, as chunk indices into a stage
+  // buffer, computed once
+  int kidx[4], vidx[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kr[c] = kb[r * kPfRowChunks + ((4 * c + grp) ^ r)];
+  for (int c = 0; c < 4; ++c) {
+    kidx[c] = r * kPfRowChunks + ((4 * c + grp) ^ r);
+    vidx[c] = kPfHalf + vt_row * kPfRowChunks + ((4 * c + (r & 3)) ^ pf_swz(vt_row));
+  }
+  auto scores = [&](const uint4* kb) {
+    uint4 kr[4];
 #pragma unroll
-      for (int tt = 0; tt < kPfTiles; ++tt) {
-        sa[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 4; ++c) kr[c] = kb[kidx[c]];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) sa[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sa[tt]);
-      }
+    for (int tt = 0; tt < kPfTiles; ++tt) {
+      sa[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kr[c] = kb[kPfPage + r * kPfRowChunks + ((4 * c + grp) ^ r)];
-#pragma unroll
-      for (int tt = 0; tt < kPfTiles; ++tt) {
-        sb[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) sb[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sb[tt]);
-      }
+      for (int c = 0; c < 4; ++c) sa[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sa[tt]);
     }
-    // online softmax over the step's 32 keys; the scale is folded into exp2's argument. The
-    // running max moves only when some key exceeds it by more than kPfSlack (log2 units):
-    // exponentials stay below 2^kPfSlack, and on most steps no lane finds such a key, so the
-    // cross-lane max, the new offsets and the rescale are skipped (a wave-uniform branch).
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kr[c] = kb[kPfPage + kidx[c]];
+#pragma unroll
+    for (int tt = 0; tt < kPfTiles; ++tt) {
+      sb[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sb[tt] = mfma_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qf[tt][c], sb[tt]);
+    }
+  };
+  // online softmax over the step's 32 keys; the scale is folded into exp2's argument. The
+  // running max moves only when some key exceeds it by more than kPfSlack (log2 units):
+  // exponentials stay below 2^kPfSlack, and on most steps no lane finds such a key, so the
+  // cross-lane max, the new offsets and the rescale are skipped (a wave-uniform branch).
+  auto softmax = [&](int s) {
+    const int key0 = s * kPfStepKeys;
     const int pos = key0 + grp * 4;
     const bool need_mask = key0 + kPfStepKeys - 1 > w_min_limit;
-    bf16x8 pf[kPfTiles];
     float x[kPfTiles][8];
     bool over = false;
 #pragma unroll
@@ -326,14 +335,16 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
       pf[tt] = __builtin_bit_cast(bf16x8, w);
       l[tt] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
     }
-    // O^T += V^T . P^T with 16x16x32 MFMAs over the step's 32 keys: lane (r, grp) carries keys
-    // 4grp..4grp+3 of both pages, the order P^T's fragment uses; V^T by transpose reads. Keys
-    // from vlim on were requested out of range, which writes zeros into LDS, so 0 * stale never
-    // reaches the sums.
-    const char* va = reinterpret_cast<const char*>(kb + kPfHalf + vt_row * kPfRowChunks);
+  };
+  // O^T += V^T . P^T with 16x16x32 MFMAs over the step's 32 keys: lane (r, grp) carries keys
+  // 4grp..4grp+3 of both pages, the order P^T's fragment uses; V^T by transpose reads. Keys
+  // from vlim on were requested out of range, which writes zeros into LDS, so 0 * stale never
+  // reaches the sums.
+  auto pv_update = [&](const uint4* kb) {
+    const char* va = reinterpret_cast<const char*>(kb);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int off = ((4 * (j >> 1) + (r & 3)) ^ pf_swz(vt_row)) * 16 + 8 * (j & 1);
+      const int off = vidx[j >> 1] * 16 + 8 * (j & 1);
       const uint2 wa = __builtin_bit_cast(
           uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(va + off)));
       const uint2 wb = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -342,6 +353,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
 #pragma unroll
       for (int tt = 0; tt < kPfTiles; ++tt) acc[tt][j] = mfma_16x16x32_bf16(vt, pf[tt], acc[tt][j]);
     }
+  };
+  auto compute = [&](const uint4* kb, int s) {
+    scores(kb);
+    softmax(s);
+    pv_update(kb);
   };
 
   // Pipeline over kPfStages LDS stage buffers (step k in buffer k % kPfStages, separate LDS

@@ -645,9 +645,10 @@ def measure_components(step, w, out, steps, plan_us):
             pw = BatchPrefillWithPagedKVCacheWrapper(torch.empty(1, device=dev), "NHD", kernel=kernel)
             pw.plan(st.qo_indptr, st.kv_indptr, st.kv_indices, st.last_page_len, 32, 8, 128, PAGE, causal=True)
             run = lambda: pw.run(st.q, st.cache, out=po)
-            for _ in range(3):
-                run()
-            times[kernel] = timed(run, min(steps, 20), stream) * 1e3
+            # sustained work first: the chunk takes ~0.5 ms, so 20 calls from idle clocks
+            # would time the clock ramp, not the kernel
+            prewarm(run, 100)
+            times[kernel] = timed(run, 20, stream) * 1e3
             del pw
         us = times["prefill"]
         # causal FLOPs: QK and PV, 2 flops per MAC, each token against its visible keys
