@@ -13,8 +13,10 @@
 //     Q fragments in registers); lane (r, grp) holds S^T[key 4grp + i][row r];
 //   * online softmax in fp32 over the 32 keys (exp2 with the scale folded into its argument,
 //     base-2 LSE), causal masking only on steps that reach a row's limit; the running max
-//     moves only when some key exceeds it by more than kPfSlack, so on most steps the
-//     cross-lane max and the rescale are skipped;
+//     moves only when some key exceeds it by more than kPfSlack, and the exponentials are
+//     taken with the current offsets first, so on most steps (no lane's sum of a row's
+//     exponentials above 2^kPfSlack) no max is computed and the cross-lane max, the rescale
+//     and a second pass of exponentials are skipped;
 //   * O^T += V^T . P^T with 8 v_mfma_f32_16x16x32_bf16 per tile: each lane's 8 keys are
 //     keys 4grp..4grp+3 of both pages (the order S^T left them in), V^T comes from LDS with
 //     transpose reads (ds_read_b64_tr_b16) and is shared by the wave's tiles.
@@ -38,6 +40,7 @@ constexpr float kNegInfP = -__builtin_huge_valf();
 #define ASPIRE_PF_RESCALE_SLACK 8
 #endif
 constexpr float kPfSlack = ASPIRE_PF_RESCALE_SLACK;
+constexpr float kPfSumLimit = float(1 << ASPIRE_PF_RESCALE_SLACK);  // 2^kPfSlack
 #ifndef ASPIRE_PF_STAGES
 #define ASPIRE_PF_STAGES 3
 #endif
@@ -92,7 +95,7 @@ struct PrefillParams {
   int64_t o_st, o_sh;
   float* lse;
   int32_t hq, group;
-  float scale_log2, inv_scale_log2;
+  float scale_log2;
   int32_t causal;
 };
 
@@ -173,12 +176,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
   // Per row (lane r of each tile): the running max m (base-2, scaled), the offset its
   // exponentials use (0 while the row has no key yet), the accumulators O^T, and this lane's
   // part of the row sum (fp32, over the lane's keys; the 4 lane groups are added at the end).
-  float m[kPfTiles], m_use[kPfTiles], l[kPfTiles], thr[kPfTiles];
+  float m[kPfTiles], m_use[kPfTiles], l[kPfTiles];
   f32x4 acc[kPfTiles][8];
 #pragma unroll
   for (int t = 0; t < kPfTiles; ++t) {
     m[t] = kNegInfP;
-    thr[t] = kNegInfP;  // (m + kPfSlack) in unscaled score units
     m_use[t] = 0.f;
     l[t] = 0.f;
 #pragma unroll
@@ -276,15 +278,17 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
     }
   };
   // online softmax over the step's 32 keys; the scale is folded into exp2's argument. The
-  // running max moves only when some key exceeds it by more than kPfSlack (log2 units):
-  // exponentials stay below 2^kPfSlack, and on most steps no lane finds such a key, so the
-  // cross-lane max, the new offsets and the rescale are skipped (a wave-uniform branch).
+  // running max moves only when some key exceeds it by more than kPfSlack (log2 units), so
+  // exponentials stay below 2^kPfSlack. They are computed with the current offsets first: a
+  // step on which no lane's sum of its 8 exponentials of a row exceeds 2^kPfSlack (so none of
+  // them does) keeps them, and only otherwise (and on the first step, which sets every row's
+  // max: key 0 is visible to every row) are the row maxima taken across lanes, the offsets
+  // moved, the accumulators rescaled and the exponentials recomputed (a wave-uniform branch).
   auto softmax = [&](int s) {
     const int key0 = s * kPfStepKeys;
     const int pos = key0 + grp * 4;
     const bool need_mask = key0 + kPfStepKeys - 1 > w_min_limit;
     float x[kPfTiles][8];
-    bool over = false;
 #pragma unroll
     for (int tt = 0; tt < kPfTiles; ++tt) {
 #pragma unroll
@@ -300,10 +304,20 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
           x[tt][4 + i] = kPage + i <= d ? x[tt][4 + i] : kNegInfP;
         }
       }
-      const float lmx = fmaxf(fmaxf(fmaxf(fmaxf(x[tt][0], x[tt][1]), x[tt][2]), fmaxf(fmaxf(x[tt][3], x[tt][4]), x[tt][5])),
-                              fmaxf(x[tt][6], x[tt][7]));
-      over |= lmx > thr[tt];
     }
+    float pv[kPfTiles][8], ps[kPfTiles];
+    auto exponentials = [&]() {
+#pragma unroll
+      for (int tt = 0; tt < kPfTiles; ++tt) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pv[tt][i] = __builtin_amdgcn_exp2f(fmaf(x[tt][i], p.scale_log2, -m_use[tt]));
+        ps[tt] = ((pv[tt][0] + pv[tt][1]) + (pv[tt][2] + pv[tt][3])) + ((pv[tt][4] + pv[tt][5]) + (pv[tt][6] + pv[tt][7]));
+      }
+    };
+    exponentials();
+    bool over = s == 0;
+#pragma unroll
+    for (int tt = 0; tt < kPfTiles; ++tt) over |= ps[tt] > kPfSumLimit;
     if (__builtin_amdgcn_ballot_w64(over) != 0) {
 #pragma unroll
       for (int tt = 0; tt < kPfTiles; ++tt) {
@@ -316,24 +330,21 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(kPfW
         const float a = __builtin_amdgcn_exp2f(m[tt] - mu);
         m[tt] = m_new;
         m_use[tt] = mu;
-        thr[tt] = (m_new + kPfSlack) * p.inv_scale_log2;
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[tt][j] *= a;
         l[tt] *= a;
       }
+      exponentials();
     }
 #pragma unroll
     for (int tt = 0; tt < kPfTiles; ++tt) {
-      float pv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) pv[i] = __builtin_amdgcn_exp2f(fmaf(x[tt][i], p.scale_log2, -m_use[tt]));
       uint4 w;
-      w.x = pack_bf16x2_rne(pv[0], pv[1]);
-      w.y = pack_bf16x2_rne(pv[2], pv[3]);
-      w.z = pack_bf16x2_rne(pv[4], pv[5]);
-      w.w = pack_bf16x2_rne(pv[6], pv[7]);
+      w.x = pack_bf16x2_rne(pv[tt][0], pv[tt][1]);
+      w.y = pack_bf16x2_rne(pv[tt][2], pv[tt][3]);
+      w.z = pack_bf16x2_rne(pv[tt][4], pv[tt][5]);
+      w.w = pack_bf16x2_rne(pv[tt][6], pv[tt][7]);
       pf[tt] = __builtin_bit_cast(bf16x8, w);
-      l[tt] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+      l[tt] += ps[tt];
     }
   };
   // O^T += V^T . P^T with 16x16x32 MFMAs over the step's 32 keys: lane (r, grp) carries keys
@@ -481,7 +492,6 @@ extern "C" int aspire_prefill_run(const aspire_prefill_args* a, void* stream) {
   p.hq = a->num_qo_heads;
   p.group = a->num_qo_heads / a->num_kv_heads;
   p.scale_log2 = a->sm_scale * 1.4426950408889634f;
-  p.inv_scale_log2 = 1.f / p.scale_log2;
   p.causal = a->causal;
   hipLaunchKernelGGL(prefill_kernel, dim3(a->total_blocks * a->num_kv_heads), dim3(kPfThreads), 0,
                      static_cast<hipStream_t>(stream), p);
