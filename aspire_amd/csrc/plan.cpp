@@ -33,7 +33,9 @@ constexpr int kMinPagesPerWave = 8;
 // (direct: 48). Per-wave finish times of config-4 launches (fitted per class) showed 1-tile
 // pages about 3-10% slower than 3-tile pages in a joint launch, whose tiles run on two waves
 // of the head; sweeping the 1-tile weight (32-35) gave 33 at every draft fraction, and the
-// 3-tile weight (28-40) 32. The direct weight comes from a sweep of 40-52 on configs 3 and 4.
+// 3-tile weight (28-40) 32. With the slack softmax (3-tile items 5% faster) 33/32/32 stayed
+// best against 3-tile 30 or 34, 2- and 3-tile 31 and 1-tile 34 on configs 1 and 4. The
+// direct weight comes from a sweep of 40-52 on configs 3 and 4.
 #ifndef ASPIRE_DIRECT_PAGE_COST
 #define ASPIRE_DIRECT_PAGE_COST 48
 #endif
@@ -43,8 +45,11 @@ constexpr int kMinPagesPerWave = 8;
 #ifndef ASPIRE_C2_PAGE_COST
 #define ASPIRE_C2_PAGE_COST 32
 #endif
+#ifndef ASPIRE_C3_PAGE_COST
+#define ASPIRE_C3_PAGE_COST 32
+#endif
 constexpr int64_t kDirectPageCost = ASPIRE_DIRECT_PAGE_COST;
-constexpr int64_t kSharedPageCost[3] = {ASPIRE_C1_PAGE_COST, ASPIRE_C2_PAGE_COST, 32};
+constexpr int64_t kSharedPageCost[3] = {ASPIRE_C1_PAGE_COST, ASPIRE_C2_PAGE_COST, ASPIRE_C3_PAGE_COST};
 
 struct Segment {
   int32_t q_start, q_len, kv_len, list_base, npages, bg, rows;
