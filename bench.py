@@ -622,10 +622,21 @@ def measure_components(step, w, out, steps, plan_us):
     uv = torch.rand(R, D + 1, generator=gs, device=dev)
     us_v = graph_timed(lambda: verify_topk_speculation(dprobs, dids, dtok, dcnt, tprobs, tids, uniforms=uv),
                        steps, stream) * 1e3
+    # the same verification at the largest top_k (candidate ids unique within a position)
+    KL = 1024
+    tprobs_l = torch.softmax(torch.randn(R, D + 1, KL, generator=gs, device=dev), -1)
+    dprobs_l = torch.softmax(torch.randn(R, D, KL, generator=gs, device=dev), -1)
+    off = torch.randint(0, 151936, (R, D + 1, 1), generator=gs, device=dev)
+    tids_l = (off + 97 * torch.arange(KL, device=dev)) % 151936
+    dids_l = tids_l[:, :D].clone()
+    dtok_l = dids_l[:, :, 0].to(torch.int32)
+    us_vl = graph_timed(lambda: verify_topk_speculation(dprobs_l, dids_l, dtok_l, dcnt, tprobs_l, tids_l,
+                                                        uniforms=uv), steps, stream) * 1e3
     res["sampling"] = {"topk_pipe_draw_us": round(us_s, 2), "rows": 208, "vocab": 151936, "top_k": 50,
                        "logits_bytes": 208 * 151936 * 2,
                        "logits_gbs": _gbs(208 * 151936 * 2, us_s),
                        "verify_us": round(us_v, 2), "verify_requests": R, "verify_drafts": D,
+                       "verify_us_top_k_1024": round(us_vl, 2),
                        "note": "20 calls per graph replay; top-k candidates + LogitsPipe(temperature 0.8, "
                                "top-p 0.9) + sampling_from_probs; verify_topk_speculation in one launch"}
     del logits
