@@ -104,6 +104,7 @@ class AttentionArgs(ctypes.Structure):
         ("dump_kv_stride", ctypes.c_int64), ("dump_num_heads", ctypes.c_int32),
         ("dump_mode_flags", ctypes.c_void_p),
         ("page_scores", ctypes.c_void_p), ("page_score_stride", ctypes.c_int64),
+        ("partial_nt", ctypes.c_int32),
     ]
 
 

@@ -43,6 +43,10 @@ from aspire_amd.backends.jit_kernels import (
 FLOAT_WORKSPACE_BYTES = 384 * 1024 * 1024
 INT_WORKSPACE_BYTES = 8 * 1024 * 1024
 PINNED_RING = 4
+# Plans of at most this many page-heads per wave are short launches whose end and merge wait on
+# the split-KV partials: run() has them stored non-temporally (config 4 at f = 1.0, 32 per
+# wave: 44.5 against 45.0 us on MI355X); longer plans keep plain stores.
+SHORT_PLAN_PAGES_PER_WAVE = 64
 
 
 def get_seq_lens(kv_indptr: torch.Tensor, kv_last_page_len: torch.Tensor, page_size: int) -> torch.Tensor:
@@ -350,6 +354,9 @@ class HolisticAttentionWrapper:
         else:
             a.class_mask = sum(1 << c for c in range(3) if info.num_items[c] > 0)
             a.launch_merge = 1 if info.num_merge > 0 else 0
+        # short plans store their split-KV partials non-temporally (a graph keeps the choice
+        # of the plan it was captured with; either is correct for any plan)
+        a.partial_nt = 1 if info.total_pages <= SHORT_PLAN_PAGES_PER_WAVE * self._layout.num_waves else 0
         keep_alive = [q, out, lse]
         wants_dump = self._has_jit and self._dump is not None and self._dump.kind != "noop"
         if (wants_dump or page_scores is not None) and info.split_rows > 0:

@@ -119,6 +119,24 @@ constexpr int kValuRows = 4;
 constexpr float kAttnSumLimit = float(1 << ASPIRE_ATTN_SLACK);  // 2^slack
 #endif
 
+// Split-KV partial rows: plain stores, or non-temporal ones in the kernel instance the host
+// launches for short plans (aspire_attention_args.partial_nt: at most 64 page-heads per wave).
+// Measured on MI355X at config 4 f = 1.0 (32 page-heads per wave): 44.5 against 45.0 us;
+// long launches measured 0.2% slower with non-temporal partials, so they keep plain stores.
+template <bool kNt>
+__device__ __forceinline__ void store_partial4(float* dst, float a, float b, float c, float d) {
+  if constexpr (kNt) {
+    f32x4 v;
+    v[0] = a;
+    v[1] = b;
+    v[2] = c;
+    v[3] = d;
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
+  } else {
+    *reinterpret_cast<float4*>(dst) = make_float4(a, b, c, d);
+  }
+}
+
 // Tile lanes. A workgroup holds kAttnWavesPerBlock kv heads (the plan's waves) x kTileLanes
 // waves: the tile lanes of a head share that head's item list, and lane tl computes the
 // 16-row tiles [tl * k, min((tl + 1) * k, tiles)) of an item of `tiles` tiles, with
@@ -316,7 +334,7 @@ struct Stager {
 // One (row, kv head) piece: this wave computes NT of its tiles, from tile tile0 (rows
 // 16 * tile0 ...). compute = false: a wave with no tile of the item, which only takes its
 // part in staging the pages (staged items) or has nothing to do (direct items).
-template <int NT, int SW, bool kStage, bool kSplitItem = false, bool kValu = false>
+template <int NT, int SW, bool kStage, bool kSplitItem = false, bool kValu = false, bool kNt = false>
 __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it, int lane,
                                          i16x4 ident, bool staged, uint4* stage_lds, int tile0, bool compute) {
   static_assert(!kValu || NT == 1, "the VALU path serves 1-tile items");
@@ -905,8 +923,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
       } else {
         const int64_t prow = int64_t(it.partial_row) + jr;
         float* dst = p.part_o + prow * kHeadDim + dim_off(grp, cr);
-        reinterpret_cast<float4*>(dst)[0] = make_float4(o0.x * inv, o0.y * inv, o0.z * inv, o0.w * inv);
-        reinterpret_cast<float4*>(dst)[1] = make_float4(o1.x * inv, o1.y * inv, o1.z * inv, o1.w * inv);
+        store_partial4<kNt>(dst, o0.x * inv, o0.y * inv, o0.z * inv, o0.w * inv);
+        store_partial4<kNt>(dst + 4, o1.x * inv, o1.y * inv, o1.z * inv, o1.w * inv);
         if (grp == 0 && cr == 0) p.part_lse[prow] = lse_v;
       }
     }
@@ -946,8 +964,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const f32x4 a = acc[t][j];
-        *reinterpret_cast<float4*>(dst + dim_off(grp, j >> 1) + 4 * (j & 1)) =
-            make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+        store_partial4<kNt>(dst + dim_off(grp, j >> 1) + 4 * (j & 1), a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
       }
       if (grp == 0) p.part_lse[prow] = lse_v;
     }
@@ -956,27 +973,27 @@ __device__ __forceinline__ void run_item(const AttnParams& p, const WorkItem& it
 
 // One item of a class for this wave: n of its tiles from tile0 (n = K or the short share R;
 // 0: no tile), kStage: the wave loads a block of the staged pages.
-template <int TILES, int K, int R, int SW, bool kStage, bool kSplit>
+template <int TILES, int K, int R, int SW, bool kStage, bool kSplit, bool kNt>
 __device__ __forceinline__ void run_class_item(const AttnParams& p, const WorkItem& it, int lane, i16x4 ident,
                                                bool stg, uint4* stage_lds, int tile0, int n) {
   if constexpr (TILES == 1 && ASPIRE_DRAFT_VALU) {
     if (it.q_len * p.group <= kValuRows) {
-      run_item<1, SW, kStage, false, true>(p, it, lane, ident, stg, stage_lds, tile0, n > 0);
+      run_item<1, SW, kStage, false, true, kNt>(p, it, lane, ident, stg, stage_lds, tile0, n > 0);
       return;
     }
   }
   if (n == K) {
-    run_item<K, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, true);
+    run_item<K, SW, kStage, kSplit, false, kNt>(p, it, lane, ident, stg, stage_lds, tile0, true);
   } else if constexpr (R > 0) {
-    if (n == R) run_item<R, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, true);
-    else run_item<K, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, false);
+    if (n == R) run_item<R, SW, kStage, kSplit, false, kNt>(p, it, lane, ident, stg, stage_lds, tile0, true);
+    else run_item<K, SW, kStage, kSplit, false, kNt>(p, it, lane, ident, stg, stage_lds, tile0, false);
   } else {
-    run_item<K, SW, kStage, kSplit>(p, it, lane, ident, stg, stage_lds, tile0, false);
+    run_item<K, SW, kStage, kSplit, false, kNt>(p, it, lane, ident, stg, stage_lds, tile0, false);
   }
 }
 
 // Items of one row-tile class (TILES 16-row tiles) for this wave, tile lane tl of its head.
-template <int TILES>
+template <int TILES, bool kNt>
 __device__ __forceinline__ void run_class(const AttnParams& p, int c, int w0, int w1, int lane, i16x4 ident,
                                           bool staged, uint4* stage_lds, int tl) {
   constexpr bool kSplit = TILES >= ASPIRE_SPLIT_MIN_TILES;
@@ -1005,9 +1022,9 @@ __device__ __forceinline__ void run_class(const AttnParams& p, int c, int w0, in
     const bool stg = staged && !(q_len_flags & kItemDirect) && K <= ASPIRE_STAGED_MAX_NT;
     constexpr bool kSplitItems = kSplit && LANES > 1;
     if (stager) {
-      run_class_item<TILES, K, R, SW, true, kSplitItems>(p, it, lane, ident, stg, stage_lds, tile0, n);
+      run_class_item<TILES, K, R, SW, true, kSplitItems, kNt>(p, it, lane, ident, stg, stage_lds, tile0, n);
     } else {
-      run_class_item<TILES, K, R, SW, false, kSplitItems>(p, it, lane, ident, stg, stage_lds, tile0, n);
+      run_class_item<TILES, K, R, SW, false, kSplitItems, kNt>(p, it, lane, ident, stg, stage_lds, tile0, n);
     }
   }
 }
@@ -1017,6 +1034,7 @@ __device__ __forceinline__ void run_class(const AttnParams& p, int c, int w0, in
 // the head waves), so the launch has one ramp and one tail. A workgroup is
 // kAttnWavesPerBlock head waves of the plan x kTileLanes tile lanes; the
 // default grid runs one head wave per SIMD (plus its tile lanes).
+template <bool kNt>
 __global__ __launch_bounds__(64 * kWgWaves)
 __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_kernel(AttnParams p) {
   const int lane = threadIdx.x & 63;
@@ -1046,9 +1064,9 @@ __attribute__((amdgpu_waves_per_eu(ASPIRE_ATTN_WAVES_PER_EU))) void attention_ke
     w0[c] = wave_uniform(indptr[wave]);
     w1[c] = wave_uniform(indptr[wave + 1]);
   }
-  if (p.class_mask & 1) run_class<1>(p, 0, w0[0], w1[0], lane, ident, staged, stage_lds, tl);
-  if (p.class_mask & 2) run_class<2>(p, 1, w0[1], w1[1], lane, ident, staged, stage_lds, tl);
-  if (p.class_mask & 4) run_class<3>(p, 2, w0[2], w1[2], lane, ident, staged, stage_lds, tl);
+  if (p.class_mask & 1) run_class<1, kNt>(p, 0, w0[0], w1[0], lane, ident, staged, stage_lds, tl);
+  if (p.class_mask & 2) run_class<2, kNt>(p, 1, w0[1], w1[1], lane, ident, staged, stage_lds, tl);
+  if (p.class_mask & 4) run_class<3, kNt>(p, 2, w0[2], w1[2], lane, ident, staged, stage_lds, tl);
 }
 
 // Merge of split segments. A task is (merge item, 4 units), one unit per 16-lane group: a
@@ -1311,7 +1329,10 @@ int attention_run_impl(const aspire_plan_layout* layout, const aspire_attention_
   }
   p.class_mask = a->class_mask & 7;
   if (p.class_mask) {
-    hipLaunchKernelGGL(attention_kernel, grid, block, 0, s, p);
+    if (a->partial_nt)
+      hipLaunchKernelGGL(attention_kernel<true>, grid, block, 0, s, p);
+    else
+      hipLaunchKernelGGL(attention_kernel<false>, grid, block, 0, s, p);
     ASPIRE_CHECK_LAUNCH();
   }
   if (a->launch_merge) {

@@ -210,6 +210,9 @@ typedef struct aspire_attention_args {
   int64_t dump_kv_stride; int32_t dump_num_heads;
   const int32_t* dump_mode_flags; /* per row, 0 disables; NULL = all rows */
   float* page_scores; int64_t page_score_stride; /* [segments, stride] or NULL */
+  int32_t partial_nt;             /* 1: store split-KV partials non-temporally (short plans,
+                                     at most 64 page-heads per wave; no reference counterpart);
+                                     0 (zero-initialised callers): plain stores */
 } aspire_attention_args;
 
 int aspire_attention_run(const aspire_plan_layout* layout,

@@ -416,3 +416,34 @@ def test_small_layout_merge_reads_stay_in_plan(gpu):
     ref, _ = paged_attention(step.q.cpu(), step.cache.cpu(), step.qo_indptr_host, step.kv_indptr_host,
                              step.kv_indices.cpu(), step.kv_len_host, num_kv_heads=step.hkv)
     attn_close(out[:T], ref[:T])
+
+
+@pytest.mark.parametrize("ctx,q_len,draft", [
+    ([20000, 9000, 2048, 15000], [1, 4, 1, 9], [0, 0, 1, 0]),   # a short plan: few pages per wave
+    ([8192] * 24, [1, 4, 9] * 8, [1, 0, 0] * 8),               # longer: ~90 page-heads per wave
+])
+def test_partial_store_kinds_are_bitwise_identical(gpu, monkeypatch, ctx, q_len, draft):
+    """run() stores the split-KV partials non-temporally for plans of at most
+    SHORT_PLAN_PAGES_PER_WAVE page-heads per wave and with plain stores otherwise; the two kernel
+    instances write the same values, so forcing either choice gives bit-equal outputs and LSEs."""
+    from aspire_amd.attention import holistic_wrapper as hw
+
+    say("partial store kinds", len(ctx))
+    step = build_step(hq=32, hkv=8, ctx_len=ctx, q_len=q_len, is_draft=draft, draft_budget=64, seed=23, device=gpu)
+    w = make_wrapper(gpu)
+    plan(w, step)
+    assert w.plan_info.num_merge > 0
+    short = w.plan_info.total_pages <= hw.SHORT_PLAN_PAGES_PER_WAVE * w._layout.num_waves
+    assert short == (len(ctx) == 4)
+    res = {}
+    for limit in (0, 1 << 30):  # plain, then non-temporal partial stores
+        monkeypatch.setattr(hw, "SHORT_PLAN_PAGES_PER_WAVE", limit)
+        out, lse = w.run(step.q, step.cache, return_lse=True)
+        torch.cuda.synchronize()
+        res[limit] = (out.clone(), lse.clone())
+    (o0, l0), (o1, l1) = res[0], res[1 << 30]
+    T = step.total_tokens
+    assert torch.equal(o0[:T].view(torch.int16), o1[:T].view(torch.int16))
+    assert torch.equal(l0[:T], l1[:T])
+    ref_out, ref_lse = oracle(step, step.cache)
+    check_rows(step, o1, l1, ref_out, ref_lse)
