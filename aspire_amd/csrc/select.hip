@@ -12,13 +12,14 @@
 //     (head, slot) and thread, 128 pages per 256-thread workgroup;
 //   * other page sizes (1..16): 16 lanes per page, one token per lane.
 //
-// topk: one wave per row / (row, kv head) segment. Scores become
-// order-preserving uint32 keys (in registers up to 2048 pages, else in LDS);
-// up to 32 steps of a bitwise search, each counting keys >= a candidate, find
-// the k-th largest key (or stop once exactly k keys are >= the candidate); an ordered compaction keeps every larger key plus the
-// lowest-index ties (mbcnt ranks), emitting logical pages in ascending order. When the reference's
-// order is requested they are sorted by physical page id: skipped when the
-// ids are already ascending, a rank sort up to 256 pages, bitonic beyond.
+// topk: one workgroup per row / (row, kv head) segment. Scores become
+// order-preserving uint32 keys held in registers; a radix select over three
+// digits (LDS histograms, one workgroup-wide scan per digit) finds the k-th
+// largest key, and an ordered compaction (one exclusive scan of per-thread
+// counts) keeps every larger key plus the lowest-index ties, emitting logical
+// pages in ascending order. When the reference's order is requested they are
+// sorted by physical page id: skipped when the ids are already ascending, a
+// rank sort up to 4 x (threads) pages, bitonic beyond.
 #include <algorithm>
 
 #include "common.h"
@@ -26,7 +27,6 @@
 namespace aspire {
 namespace {
 
-constexpr int kTopkThreads = 64;
 constexpr int kMaxSel = 2048;
 
 struct ScoreParams {
@@ -137,14 +137,6 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ int popc64(uint64_t m) { return __builtin_popcountll(m); }
-
-// Number of set bits of m in lanes below this one.
-__device__ __forceinline__ int lanes_below(uint64_t m) {
-  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-}
-
 struct TopkParams {
   const float* scores;
   int64_t score_stride;
@@ -163,55 +155,9 @@ struct TopkParams {
   int32_t* valid;
 };
 
-// Keys of one segment, lane l holding keys 256 i + 4 l + e (e < 4) of step i.
-// KREG > 0: the keys live in KREG registers per lane (n_pad <= 64 * KREG);
-// KREG == 0: they stay in LDS and every pass reads them back.
-template <int KREG>
-struct SegmentKeys {
-  uint32_t reg[KREG > 0 ? KREG : 1];
-  const uint32_t* lds;
-  int n_pad;
-
-  __device__ __forceinline__ uint4 quad(int i) const {
-    if constexpr (KREG > 0) {
-      return uint4{reg[4 * i], reg[4 * i + 1], reg[4 * i + 2], reg[4 * i + 3]};
-    } else {
-      return *reinterpret_cast<const uint4*>(lds + 256 * i + 4 * threadIdx.x);
-    }
-  }
-  __device__ __forceinline__ int steps() const { return n_pad >> 8; }
-
-  // Wave-wide count of keys >= cand (padding keys are 0 and cand >= 1),
-  // counted per lane in VALU and summed once (a ballot + scalar popcount per
-  // key stalls on every vector-to-scalar dependency).
-  __device__ __forceinline__ int count_ge(uint32_t cand) const {
-    int cnt = 0;
-    if constexpr (KREG > 0) {
-      // All KREG registers hold keys (0 past n): no per-step guard, no branch.
-#pragma unroll
-      for (int i = 0; i < KREG / 4; ++i) {
-        const uint4 q = quad(i);
-        cnt += int(q.x >= cand) + int(q.y >= cand) + int(q.z >= cand) + int(q.w >= cand);
-      }
-    } else {
-      for (int i = 0; i < steps(); ++i) {
-        const uint4 q = quad(i);
-        cnt += int(q.x >= cand) + int(q.y >= cand) + int(q.z >= cand) + int(q.w >= cand);
-      }
-    }
-    return wave_sum_int(cnt);
-  }
-};
-
-template <int KREG>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
-  extern __shared__ __align__(16) uint32_t keys[];
-  __shared__ __align__(16) int32_t sel[kMaxSel];
-  const int s = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int rl = s / p.segs_per_row;
-  const int row = p.row_ids ? p.row_ids[rl] : rl;
-  const int n = min(max(p.num_pages[row], 0), static_cast<int>(p.score_stride));
+// Pages a segment of n pages keeps (page_selector.py:52-62): the budget, the minimum, or
+// the percentage clamped between them.
+__device__ __forceinline__ int segment_take(const TopkParams& p, int n) {
   int k;
   if (p.count_mode == 0) {
     k = min(n, p.subset);
@@ -222,115 +168,155 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
     const float t = ceilf((static_cast<float>(n) * p.pct) / 100.0f);
     k = min(max(static_cast<int>(t), lo), hi);
   }
-  k = max(k, 0);
+  return max(k, 0);
+}
+
+// One workgroup per segment (a row or a (row, kv head)); thread t holds the keys of pages
+// PER t .. PER t + PER - 1 in registers (THREADS x PER >= the score stride: 256 x 8 up to
+// 2,048 pages, 1,024 x 12 up to 12,288). The k-th largest key comes from a radix select over
+// 11-, 11- and 10-bit digits (bits 31..21, 20..10, 9..0): each pass counts the keys that
+// match the digits chosen so far in an LDS histogram of 2,048 bins, and one workgroup-wide
+// scan over the bins in descending order finds the digit whose bin holds the k-th key. A
+// pass whose bin holds exactly the keys still needed ends the search (every key >= the
+// bin's lowest value is taken). The compaction is one workgroup-wide exclusive scan of each
+// thread's (keys above, ties) counts: a thread writes its taken pages at its offset, in page
+// order, ties by lowest page first.
+constexpr int kTbBins = 2048;
+
+// Exclusive prefix sum of v over the workgroup's threads in index order (inclusive
+// shuffles within each wave, wave totals through LDS); *total gets the sum of all.
+template <int THREADS>
+__device__ __forceinline__ uint32_t tb_exclusive_scan(uint32_t v, uint32_t* wtot, uint32_t* total) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) wtot[w] = inc;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < THREADS / 64; ++i) {
+    const uint32_t x = wtot[i];
+    before += i < w ? x : 0u;
+    all += x;
+  }
+  __syncthreads();  // wtot is reused by the next scan
+  *total = all;
+  return before + inc - v;
+}
+
+template <int THREADS, int PER>
+__global__ __launch_bounds__(THREADS) void topk_block_kernel(TopkParams p) {
+  constexpr int BPT = kTbBins / THREADS;  // histogram bins per thread
+  static_assert(BPT * THREADS == kTbBins && THREADS * PER < 65536, "bins split evenly; counts pack into 16 bits");
+  __shared__ uint32_t hist[kTbBins];
+  __shared__ __align__(16) int32_t sel[kMaxSel];
+  __shared__ uint32_t wtot[THREADS / 64];
+  __shared__ uint32_t pick[3];  // bin, keys in higher bins, keys in the bin
+  const int s = blockIdx.x;
+  const int t = threadIdx.x;
+  const int rl = s / p.segs_per_row;
+  const int row = p.row_ids ? p.row_ids[rl] : rl;
+  const int n = min(max(p.num_pages[row], 0), static_cast<int>(p.score_stride));
+  const int k = segment_take(p, n);
   const int kk = min(min(k, kMaxSel), p.sel_width);
   const float* sc = p.scores + int64_t(s) * p.score_stride;
   const int forced_from = n - p.L;
   const uint32_t inf_key = order_key(__builtin_huge_valf());
-  SegmentKeys<KREG> K;
-  K.n_pad = (n + 255) & ~255;
-  K.lds = keys;
-  // Loads use a clamped index, so they are unconditional and all in flight at
-  // once (a guarded load becomes a branch that waits for each load in turn).
   const int last = max(n - 1, 0);
-  auto key_of = [&](int j, float v) {
-    uint32_t key = order_key(v);  // selects, not branches: the loads stay unconditional
-    key = j >= forced_from ? inf_key : key;
-    return j >= n ? 0u : key;
-  };
-  if constexpr (KREG > 0) {
-    // Padding keys are 0, below every candidate of the search.
-    float v[KREG];
+  const int j0 = PER * t;
+  // unconditional loads (clamped index): all in flight at once
+  float v[PER];
 #pragma unroll
-    for (int i = 0; i < KREG / 4; ++i) {
+  for (int e = 0; e < PER; ++e) v[e] = sc[min(j0 + e, last)];
+  for (int i = t; i < kTbBins; i += THREADS) hist[i] = 0u;
+  uint32_t key[PER];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[4 * i + e] = sc[min(256 * i + 4 * lane + e, last)];
-    }
-#pragma unroll
-    for (int i = 0; i < KREG / 4; ++i) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) K.reg[4 * i + e] = key_of(256 * i + 4 * lane + e, v[4 * i + e]);
-    }
-  } else {
-    // Eight independent loads in flight per lane before the LDS writes.
-    for (int j0 = 0; j0 < K.n_pad; j0 += 8 * kTopkThreads) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = sc[min(j0 + u * kTopkThreads + lane, last)];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u * kTopkThreads + lane;
-        if (j < K.n_pad) keys[j] = key_of(j, v[u]);
-      }
-    }
-    __syncthreads();
-  }
-  // thr = the kk-th largest key: the largest value with count(key >= thr) >= kk.
-  uint32_t thr = 0;
-  int need_eq = n;  // kk == n: every key is taken
+  for (int e = 0; e < PER; ++e) key[e] = j0 + e >= forced_from ? inf_key : order_key(v[e]);
+
+  // thr and need_eq: take every page with key > thr, and the first need_eq pages with key == thr
+  uint32_t thr = 0u;
+  int need_eq = n;  // kk == n: every page is taken
+  uint32_t total = 0u;
   if (kk > 0 && kk < n) {
+    uint32_t prefix = 0u, hi_mask = 0u;
+    int need = kk;
     bool exact = false;
-    for (int b = 31; b >= 0; --b) {
-      const uint32_t cand = thr | (1u << b);
-      const int c = K.count_ge(cand);
-      if (c >= kk) thr = cand;
-      if (c == kk) {  // exactly the keys >= cand are selected: stop early
+    __syncthreads();  // histogram cleared
+#pragma unroll
+    for (int pass = 0; pass < 3; ++pass) {
+      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+      const uint32_t dmask = pass == 2 ? 1023u : 2047u;
+#pragma unroll
+      for (int e = 0; e < PER; ++e)
+        if (j0 + e < n && (key[e] & hi_mask) == prefix) atomicAdd(&hist[(key[e] >> shift) & dmask], 1u);
+      __syncthreads();
+      // thread t reads (and clears for the next pass) bins dmask - BPT t - i, i < BPT: the
+      // workgroup's threads in index order cover the bins in descending order
+      uint32_t c[BPT];
+      uint32_t local = 0u;
+#pragma unroll
+      for (int i = 0; i < BPT; ++i) {
+        const int b = int(dmask) - BPT * t - i;
+        c[i] = b >= 0 ? hist[b] : 0u;
+        if (b >= 0) hist[b] = 0u;
+        local += c[i];
+      }
+      uint32_t above = tb_exclusive_scan<THREADS>(local, wtot, &total);
+      if (above < uint32_t(need) && above + local >= uint32_t(need)) {
+#pragma unroll
+        for (int i = 0; i < BPT; ++i) {
+          if (above + c[i] >= uint32_t(need)) {
+            pick[0] = uint32_t(int(dmask) - BPT * t - i);
+            pick[1] = above;
+            pick[2] = c[i];
+            break;
+          }
+          above += c[i];
+        }
+      }
+      __syncthreads();
+      const uint32_t b = pick[0];
+      need -= int(pick[1]);
+      const int in_bin = int(pick[2]);
+      prefix |= b << shift;
+      hi_mask |= dmask << shift;
+      if (in_bin == need && prefix != 0u) {
         exact = true;
         break;
       }
     }
     if (exact) {
-      thr -= 1u;  // take key > cand - 1, i.e. key >= cand (cand >= 1); no ties needed
+      thr = prefix - 1u;  // key > prefix - 1: every key >= the bin's lowest value
       need_eq = 0;
     } else {
-      const int gt = thr == 0xffffffffu ? 0 : K.count_ge(thr + 1u);
-      need_eq = kk - gt;
+      thr = prefix;
+      need_eq = need;
     }
   }
-  // Ordered compaction: every key above thr, plus the lowest-index ties.
-  int base = 0, eq_base = 0;
-  auto compact_step = [&](int i) {
-    const int jl = 256 * i + lane * 4;
-    const uint4 k4 = K.quad(i);
-    const uint32_t kv[4] = {k4.x, k4.y, k4.z, k4.w};
-    bool eq[4], gt[4];
-    uint64_t eqm[4];
-    int eq_below = 0;
+  // ordered compaction
+  uint32_t gt = 0u, eq = 0u;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool in = jl + e < n;
-      eq[e] = in && kv[e] == thr;
-      gt[e] = in && kv[e] > thr;
-      eqm[e] = __builtin_amdgcn_ballot_w64(eq[e]);
-      eq_below += lanes_below(eqm[e]);
-    }
-    bool take[4];
-    uint64_t tm[4];
-    int take_below = 0;
-    int rank = eq_base + eq_below;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      take[e] = gt[e] || (eq[e] && rank < need_eq);
-      rank += eq[e];
-      tm[e] = __builtin_amdgcn_ballot_w64(take[e]);
-      take_below += lanes_below(tm[e]);
-    }
-    int pos = base + take_below;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (take[e] && pos < kMaxSel) sel[pos] = jl + e;
-      pos += take[e];
-      base += popc64(tm[e]);
-      eq_base += popc64(eqm[e]);
-    }
-  };
+  for (int e = 0; e < PER; ++e) {
+    const bool in = j0 + e < n;
+    gt += uint32_t(in && key[e] > thr);
+    eq += uint32_t(in && key[e] == thr);
+  }
+  const uint32_t ex = tb_exclusive_scan<THREADS>(gt | (eq << 16), wtot, &total);
   if (kk > 0) {
-    if constexpr (KREG > 0) {
+    int eq_rank = int(ex >> 16);
+    int pos = int(ex & 0xffffu) + min(eq_rank, need_eq);
 #pragma unroll
-      for (int i = 0; i < KREG / 4; ++i)  // constant register indices
-        if (i < K.steps() && base < kk) compact_step(i);
-    } else {
-      for (int i = 0; i < K.steps() && base < kk; ++i) compact_step(i);
+    for (int e = 0; e < PER; ++e) {
+      const bool in = j0 + e < n;
+      const bool tie = in && key[e] == thr;
+      const bool take = (in && key[e] > thr) || (tie && eq_rank < need_eq);
+      eq_rank += int(tie);
+      if (take && pos < kMaxSel) sel[pos] = j0 + e;
+      pos += int(take);
     }
   }
   __syncthreads();
@@ -338,25 +324,22 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
   // Map logical -> physical; pad with INT_MAX to a power of two >= 4 for the sorts.
   int pow2 = 4;
   while (pow2 < kk) pow2 <<= 1;
-  for (int i = lane; i < pow2; i += kTopkThreads)
+  for (int i = t; i < pow2; i += THREADS)
     sel[i] = i < kk ? trow[max(0, min(sel[i], static_cast<int>(p.table_stride) - 1))] : 0x7fffffff;
   __syncthreads();
   if (p.order == 0 && kk > 1) {
-    // Already ascending (the reference's arange block table): nothing to do.
     bool desc = false;
-    for (int i = lane; i + 1 < kk; i += kTopkThreads) desc |= sel[i] > sel[i + 1];
-    if (__builtin_amdgcn_ballot_w64(desc) != 0) {
-      if (kk <= 4 * kTopkThreads) {
-        // Rank sort: lane l places entries l + 64u at their rank, read with
-        // broadcast LDS loads (ties keep index order; equal ids are identical).
-        // Lexicographic (id, index) keys make every rank distinct; entries
-        // [kk, pad4) hold INT_MAX with indices >= kk, so they rank above all.
-        const int per = (kk + kTopkThreads - 1) / kTopkThreads;
+    for (int i = t; i + 1 < kk; i += THREADS) desc |= sel[i] > sel[i + 1];
+    if (__syncthreads_or(desc)) {
+      if (kk <= 4 * THREADS) {
+        // Rank sort: thread t places entries t + THREADS u at their rank, read with broadcast LDS
+        // loads; lexicographic (id, index) keys make every rank distinct.
+        const int per = (kk + THREADS - 1) / THREADS;
         int64_t mine[4];
         int rank[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int i = lane + 64 * u;
+          const int i = t + THREADS * u;
           mine[u] = (int64_t(i < kk ? sel[i] : 0x7fffffff) << 32) | i;
           rank[u] = 0;
         }
@@ -375,12 +358,12 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-          if (lane + 64 * u < kk) sel[rank[u]] = int32_t(mine[u] >> 32);
+          if (t + THREADS * u < kk) sel[rank[u]] = int32_t(mine[u] >> 32);
         __syncthreads();
       } else {
         for (int size = 2; size <= pow2; size <<= 1) {
           for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = lane; i < pow2; i += kTopkThreads) {
+            for (int i = t; i < pow2; i += THREADS) {
               const int partner = i ^ stride;
               if (partner > i) {
                 const bool up = (i & size) == 0;
@@ -398,8 +381,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
     }
   }
   int32_t* out = p.selected + int64_t(s) * p.sel_stride;
-  for (int i = lane; i < p.sel_width; i += kTopkThreads) out[i] = i < kk ? sel[i] : 0;
-  if (lane == 0 && p.valid != nullptr) p.valid[s] = k;
+  for (int i = t; i < p.sel_width; i += THREADS) out[i] = i < kk ? sel[i] : 0;
+  if (t == 0 && p.valid != nullptr) p.valid[s] = k;
 }
 
 }  // namespace
@@ -491,12 +474,10 @@ extern "C" int aspire_select_topk(const float* scores, int64_t score_stride, con
   p.sel_width = sel_width;
   p.valid = valid;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (score_stride <= 64 * 32) {  // keys in 32 registers per lane
-    hipLaunchKernelGGL(topk_kernel<32>, dim3(segments), dim3(kTopkThreads), 0, st, p);
-  } else {
-    const size_t lds = size_t((score_stride + 255) & ~int64_t(255)) * 4;
-    hipLaunchKernelGGL(topk_kernel<0>, dim3(segments), dim3(kTopkThreads), lds, st, p);
-  }
+  if (score_stride <= 256 * 8)
+    hipLaunchKernelGGL((topk_block_kernel<256, 8>), dim3(segments), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((topk_block_kernel<1024, 12>), dim3(segments), dim3(1024), 0, st, p);
   ASPIRE_CHECK_LAUNCH();
   return ASPIRE_OK;
 }

@@ -328,6 +328,54 @@ def test_topk_kernel_exact_with_ties_and_wide_rows(gpu, order, stride):
         assert not got[s, k:].any()
 
 
+@pytest.mark.parametrize("order", [0, 1])
+def test_topk_kernel_radix_digits(gpu, order):
+    """Key sets that walk every digit of the radix select (rows of up to 2,048 pages): keys
+    that differ only in their low 10 bits, ties straddling the k-th key in each digit, an
+    all-equal row, signed zeros, negative-only rows, the forced last pages, and budgets of
+    0, 1, n - 1 and n."""
+    say("topk radix digits", order)
+    rng = np.random.default_rng(23 + order)
+    stride = 2048
+    base = np.float32(1.0)
+    ulps = (base.view(np.uint32) + np.arange(stride, dtype=np.uint32)).view(np.float32)
+    rows = [
+        rng.permutation(ulps),                                       # keys differ in bits 0..10 only
+        np.repeat(rng.permutation(ulps[:64]), 32),                   # 32-fold ties, low bits
+        np.full(stride, 3.5, dtype=np.float32),                      # one value
+        rng.choice(np.array([0.0, -0.0, 1e-30, -1e-30], dtype=np.float32), stride),
+        -np.abs(rng.standard_normal(stride)).astype(np.float32),     # negative only
+        (rng.integers(0, 3, stride) * np.float32(2.0) ** 20).astype(np.float32),  # ties in the top digit
+        rng.standard_normal(stride).astype(np.float32),
+        (ulps * np.where(rng.random(stride) < 0.5, 1, 1024)).astype(np.float32),  # two clusters
+    ]
+    scores = np.stack(rows).astype(np.float32)
+    segs = scores.shape[0]
+    table = np.stack([rng.permutation(stride).astype(np.int32) for _ in range(segs)])
+    sd, td = (torch.from_numpy(a).to(gpu) for a in (scores, table))
+    for npg_list, L, subset in (([2048, 2048, 2048, 2048, 2048, 2048, 2048, 2048], 0, 128),
+                                ([2048, 1700, 513, 2000, 1999, 2048, 1024, 777], 5, 700),
+                                ([2048, 2, 1, 2048, 3, 129, 2048, 64], 0, 2047),
+                                ([128, 2048, 16, 1000, 2048, 2048, 1, 100], 2, 1)):
+        npg = np.array(npg_list, dtype=np.int32)
+        width = subset
+        sel = torch.full((segs, width), -1, dtype=torch.int32, device=gpu)
+        valid = torch.zeros(segs, dtype=torch.int32, device=gpu)
+        nd = torch.from_numpy(npg).to(gpu)
+        _lib.check(_lib.lib().aspire_select_topk(_lib.ptr(sd), stride, _lib.ptr(nd), None, segs, 1, L, 0, subset, 0,
+                                                 0.0, _lib.ptr(td), stride, order, _lib.ptr(sel), width, width,
+                                                 _lib.ptr(valid), _lib.stream_of(sd)), "topk")
+        torch.cuda.synchronize()
+        got, got_valid = sel.cpu().numpy(), valid.cpu().numpy()
+        for s in range(segs):
+            n = int(npg[s])
+            k = min(n, subset)
+            assert got_valid[s] == k
+            exp = _topk_expected(scores[s], n, L, k, table[s], order)
+            assert np.array_equal(got[s, :k], exp), (npg_list, s)
+            assert not got[s, k:].any()
+
+
 def test_topk_kernel_width_clamp_and_percent_count(gpu):
     rng = np.random.default_rng(5)
     segs, stride = 4, 4096
