@@ -9,7 +9,7 @@
 // (the reference maps it to -inf, whose exp2 is 0 and never wins the max over
 // values >= 0), and exp2(+-inf) equals exp2(+-FLT_MAX) in fp32.
 //   * page 16, 8-aligned strides: 2 threads per page, one 16-byte load per
-//     (head, slot) and thread, 128 pages per 256-thread workgroup;
+//     (head, slot) and thread, 32 pages per one-wave workgroup;
 //   * other page sizes (1..16): 16 lanes per page, one token per lane.
 //
 // topk: one workgroup per row / (row, kv head) segment. Scores become
@@ -50,6 +50,10 @@ __device__ __forceinline__ float chain_diff(_Float16 logit, float c, float lse) 
   return static_cast<float>(prod) - lse;
 }
 
+// Pages per workgroup of the page-size-16 scores kernel (two threads per page, one wave):
+// measured 30.2 us against 32.0 for 128 pages in 256-thread workgroups at refresh scale.
+constexpr int kScPages = 32;
+
 __device__ __forceinline__ int slot_qrow(const ScoreParams& p, int row, int slot, int slots) {
   const int max_q = max(p.lse_rows - 1, 0);
   const int first = min(max(p.qo_indptr[row], 0), max_q);
@@ -57,13 +61,13 @@ __device__ __forceinline__ int slot_qrow(const ScoreParams& p, int row, int slot
   return (slot == 0 && slots == 2) ? first : last;
 }
 
-// Page size 16: thread pair (2i, 2i+1) covers page blockIdx.y * 128 + i.
+// Page size 16: thread pair (2i, 2i+1) covers page blockIdx.y * kScPages + i.
 template <int SLOTS>
-__global__ __launch_bounds__(256) void first_last_scores_p16_kernel(ScoreParams p) {
+__global__ __launch_bounds__(2 * kScPages) void first_last_scores_p16_kernel(ScoreParams p) {
   const int rl = blockIdx.x;
   const int row = p.row_ids ? p.row_ids[rl] : rl;
   const int np = p.num_pages[row];
-  const int j = blockIdx.y * 128 + (threadIdx.x >> 1);
+  const int j = blockIdx.y * kScPages + (threadIdx.x >> 1);
   if (j >= np || j >= p.pages) return;  // both threads of a page leave together
   const int t0 = j * 16 + (threadIdx.x & 1) * 8;
   float tok[8];
@@ -426,11 +430,12 @@ extern "C" int aspire_select_first_last_scores(const void* dump, int64_t kv_stri
   const bool vec = page_size == 16 && kv_stride % 8 == 0 && max_seq_length % 8 == 0 &&
                    (reinterpret_cast<uintptr_t>(dump) & 15) == 0;
   if (vec) {
-    const dim3 grid(rows, (pages + 127) / 128);
+    const dim3 grid(rows, (pages + kScPages - 1) / kScPages);
+    const dim3 block(2 * kScPages);
     if (slots == 2)
-      hipLaunchKernelGGL(first_last_scores_p16_kernel<2>, grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL(first_last_scores_p16_kernel<2>, grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL(first_last_scores_p16_kernel<1>, grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL(first_last_scores_p16_kernel<1>, grid, block, 0, st, p);
   } else {
     hipLaunchKernelGGL(first_last_scores_kernel, dim3(rows, (pages + 15) / 16), dim3(256), 0, st, p);
   }
