@@ -972,7 +972,7 @@ def _cpu_time(fn, warmup: int, runs: int):
 
 def run_cpu_baseline(step, config: int, runs: int):
     """The CPU oracle (torch fp32 attention, numpy append, key-mean scores and top-k) on the host
-    cores, per BASELINE.md's protocol: 2 warm-up runs, then the median of ``runs`` (>= 5) runs on
+    cores: 2 warm-up runs, then the median of ``runs`` (>= 5) runs on
     identical seeded inputs. Config 0 whole; config 1 whole (the bench workload: append +
     attention); config 2 on a bounded sample of 16 of its 64 rows (attention + key-mean scores +
     top-128), scaled to GB/s. Threads: the process's CPU share (OMP_NUM_THREADS, 16 on the GPU
