@@ -1349,7 +1349,9 @@ int attention_run_impl(const aspire_plan_layout* layout, const aspire_attention_
     mp.hq = p.hq;
     mp.group = p.group;
     mp.max_merge = layout->max_merge;
-    hipLaunchKernelGGL(merge_kernel, dim3(1024), dim3(256), 0, s, mp);
+    // 8,192 waves: a config-3 layer's 512 items x 12 tasks get a wave each (with 4,096 the
+    // merge took 7.2 us there, 6.2 us now); waves past the tasks exit after one load
+    hipLaunchKernelGGL(merge_kernel, dim3(2048), dim3(256), 0, s, mp);
     ASPIRE_CHECK_LAUNCH();
   }
   return ASPIRE_OK;
